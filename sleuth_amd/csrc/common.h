@@ -1,0 +1,117 @@
+// Device helpers shared by the FORGE attention kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace forge {
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+// ---------------------------------------------------------------- element conversion
+template <typename T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f32(float x) { return (T)x; }
+
+// 16 bytes of T unpacked to fp32 (VEC = 16 / sizeof(T) values).
+template <typename T> struct Vec16 {
+  static constexpr int N = 16 / sizeof(T);
+};
+
+template <typename T>
+__device__ __forceinline__ void unpack16(const uint4& raw, float* out) {
+  const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+  for (int i = 0; i < Vec16<T>::N; ++i) out[i] = to_f32<T>(e[i]);
+}
+
+template <typename T>
+__device__ __forceinline__ uint4 pack16(const float* in) {
+  uint4 raw;
+  T* e = reinterpret_cast<T*>(&raw);
+#pragma unroll
+  for (int i = 0; i < Vec16<T>::N; ++i) e[i] = from_f32<T>(in[i]);
+  return raw;
+}
+
+__device__ __forceinline__ uint4 load16(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+__device__ __forceinline__ void store16(void* p, const uint4& v) {
+  *reinterpret_cast<uint4*>(p) = v;
+}
+
+// ---------------------------------------------------------------- cross-lane sums
+// DPP lane permutations (GCN/CDNA dpp_ctrl encodings).
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <-> 7-i within each 8
+constexpr int kDppRowMirror = 0x140;      // lane i <-> 15-i within each 16
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Partner value across lane distance 2^k of an aligned group, for the butterfly steps
+// below. Steps 1 and 2 swap within quads, steps 4 and 8 mirror the 8- and 16-lane
+// halves (after the earlier steps all lanes of a quad / 8 hold the same value, so a
+// mirror pairs each lane with the other half exactly like an xor would).
+template <int STEP>
+__device__ __forceinline__ float butterfly_partner(float v) {
+  if constexpr (STEP == 1) return dpp<kDppQuadXor1>(v);
+  else if constexpr (STEP == 2) return dpp<kDppQuadXor2>(v);
+  else if constexpr (STEP == 4) return dpp<kDppRowHalfMirror>(v);
+  else if constexpr (STEP == 8) return dpp<kDppRowMirror>(v);
+  else return __shfl_xor(v, STEP, kWave);
+}
+
+// All-reduce over aligned groups of W lanes (W a power of two <= 64): every lane of
+// the group ends with the same value, since each butterfly step adds the same two
+// operands on both partner lanes (a + b == b + a in IEEE arithmetic).
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (W >= 2) v += butterfly_partner<1>(v);
+  if constexpr (W >= 4) v += butterfly_partner<2>(v);
+  if constexpr (W >= 8) v += butterfly_partner<4>(v);
+  if constexpr (W >= 16) v += butterfly_partner<8>(v);
+  if constexpr (W >= 32) v += butterfly_partner<16>(v);
+  if constexpr (W >= 64) v += butterfly_partner<32>(v);
+  return v;
+}
+
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (W >= 2) v = fmaxf(v, butterfly_partner<1>(v));
+  if constexpr (W >= 4) v = fmaxf(v, butterfly_partner<2>(v));
+  if constexpr (W >= 8) v = fmaxf(v, butterfly_partner<4>(v));
+  if constexpr (W >= 16) v = fmaxf(v, butterfly_partner<8>(v));
+  if constexpr (W >= 32) v = fmaxf(v, butterfly_partner<16>(v));
+  if constexpr (W >= 64) v = fmaxf(v, butterfly_partner<32>(v));
+  return v;
+}
+
+// exp2 that maps -inf to exactly 0 and never sees (-inf) - (-inf).
+__device__ __forceinline__ float exp2_masked(float s, float m) {
+  return s == kNegInf ? 0.0f : exp2f(s - m);
+}
+
+// Rescale factor of a running (max, sum) pair when the max moves from m_old to m_new.
+__device__ __forceinline__ float rescale(float m_old, float m_new) {
+  return m_old == kNegInf ? 0.0f : exp2f(m_old - m_new);
+}
+
+// Base position of batch row b (see include/forge_attn.h).
+__device__ __forceinline__ int64_t row_base(const int32_t* row_pos, const int64_t* pos_dev,
+                                            int64_t pos0, int b) {
+  if (row_pos) return (int64_t)row_pos[b];
+  if (pos_dev) return *pos_dev;
+  return pos0;
+}
+
+}  // namespace forge

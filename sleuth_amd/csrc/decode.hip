@@ -1,0 +1,510 @@
+// Split-K ("flash-decoding") attention for decode, speculative verify and every other
+// small-T or fp32 call (include/forge_attn.h: forge_attn_decode).
+//
+// Work split. For one (batch row b, KV head) the G = H/K query heads times the T new
+// queries form G*T "rows" (query-major: row = t*G + head-in-group); a block takes ROWS
+// of them (the GQA fan-out: every K/V row is loaded once and used for all ROWS rows,
+// in registers) and one chunk of `chunk` keys at absolute positions
+// [c*chunk, (c+1)*chunk). Grid = (chunks, K * row-blocks, B).
+//
+// Inside a block, LPR = D / VEC lanes share one key row: each lane loads 16 bytes
+// (VEC elements) of K and of V with one 128-bit load, so a group of LPR lanes reads a
+// whole row and a wave reads 64 / LPR consecutive rows - fully coalesced. Each group
+// takes NK consecutive keys per iteration (all loads issued before any math), scores
+// them with a DPP butterfly sum over its LPR lanes, and keeps an online-softmax state
+// (m, l, o) per row. The groups are then merged (xor-shuffles inside a wave, LDS across
+// the 4 waves, in a fixed order), and the block writes either the final output (the
+// row sees only this chunk) or an fp32 partial (m, l, o) for the combine kernel.
+//
+// Determinism: the key -> (group, slot) assignment depends only on the key's absolute
+// position, a key outside a row's visible range is an exact no-op on that row's state
+// (score -inf -> weight 0, max unchanged -> rescale 2^0 = 1), and merges run in a fixed
+// order. So a row's output does not depend on T or on the other rows in the call: a
+// verify row equals the decode of that token alone, bit for bit (same chunk).
+#include <limits.h>
+
+#include "common.h"
+#include "forge_internal.h"
+
+namespace forge {
+
+constexpr int kSplitThreads = 256;
+constexpr int kSplitNK = 4;  // keys per group per iteration
+constexpr int kMaxChunk = 512;
+
+struct SplitParams {
+  const void* q;
+  int64_t sqb, sqh, sqt;
+  const float* qw;
+  float eps;
+  int flags;
+  const float* cos;
+  const float* sin;
+  int64_t csb, cst;
+  const void* kc;
+  const void* vc;
+  int64_t skb, skh, sks;
+  int64_t max_len;
+  const int32_t* row_pos;
+  const int64_t* pos_dev;
+  int64_t pos0;
+  int B, T, H, K, G;
+  int rows_total;  // G * T
+  int window;
+  float scale_log2;  // softmax scale * log2(e)
+  int chunk;
+  int max_chunks;
+  void* out;
+  int64_t sob, sot, soh;
+  float2* ws_ml;  // [B*H*T][max_chunks] (m, l)
+  float* ws_o;    // [B*H*T][max_chunks][D]
+};
+
+// Visible key range [kmin, kmax] of the query at absolute position qpos.
+__device__ __forceinline__ void visible_range(int64_t qpos, int window, int64_t max_len,
+                                              int64_t& kmin, int64_t& kmax) {
+  kmax = qpos < max_len - 1 ? qpos : max_len - 1;
+  kmin = window > 0 ? qpos - window + 1 : 0;
+  if (kmin < 0) kmin = 0;
+}
+
+// Loads one q row slice (VEC values at li*VEC), with the optional fused RMSNorm + RoPE,
+// rounded once to T (the dtype the reference's q has when SDPA reads it).
+template <typename T, int D, int VEC, int LPR>
+__device__ __forceinline__ void load_q_row(const SplitParams& p, int b, int h, int t, int li,
+                                           float* q) {
+  const T* src = static_cast<const T*>(p.q) + b * p.sqb + h * p.sqh + t * p.sqt + li * VEC;
+  unpack16<T>(load16(src), q);
+  if (p.flags & FORGE_NORM_QK) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) ss += q[e] * q[e];
+    ss = group_sum<LPR>(ss);
+    const float rs = rsqrtf(ss / (float)D + p.eps);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) q[e] *= rs;
+    if (p.qw) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) q[e] *= p.qw[li * VEC + e];
+    }
+  }
+  if (p.flags & FORGE_ROPE) {
+    // NEOX pairing c <-> c + D/2: the partner slice is in lane li ^ (LPR/2).
+    const float* cr = p.cos + b * p.csb + t * p.cst + li * VEC;
+    const float* sr = p.sin + b * p.csb + t * p.cst + li * VEC;
+    const bool first_half = li < LPR / 2;
+    float y[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float partner = __shfl_xor(q[e], LPR / 2, kWave);
+      y[e] = first_half ? q[e] * cr[e] - partner * sr[e] : q[e] * cr[e] + partner * sr[e];
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) q[e] = y[e];
+  }
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) q[e] = to_f32<T>(from_f32<T>(q[e]));
+}
+
+template <typename T, int D, int ROWS>
+__global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int LPR = D / VEC;  // lanes per key row
+  static_assert(LPR >= 2 && LPR <= kWave && (LPR & (LPR - 1)) == 0, "bad head dim");
+  constexpr int NG = kSplitThreads / LPR;  // key groups per block
+  constexpr int GPW = kWave / LPR;         // key groups per wave
+  constexpr int NK = kSplitNK;
+  constexpr int KPI = NG * NK;  // keys per block iteration
+  constexpr int NWAVES = kSplitThreads / kWave;
+
+  __shared__ float sh_o[NWAVES][ROWS][D];
+  __shared__ float sh_m[NWAVES][ROWS];
+  __shared__ float sh_l[NWAVES][ROWS];
+
+  const int tid = threadIdx.x;
+  const int li = tid % LPR;
+  const int g = tid / LPR;
+  const int wave = tid / kWave;
+  const int c = blockIdx.x;
+  const int kvh = blockIdx.y % p.K;
+  const int rb = blockIdx.y / p.K;
+  const int b = blockIdx.z;
+
+  const int64_t base = row_base(p.row_pos, p.pos_dev, p.pos0, b);
+
+  // Rows of this block and their visible key ranges.
+  int64_t kmin[ROWS], kmax[ROWS];
+  int hrow[ROWS], trow[ROWS];
+  bool valid[ROWS];
+  int64_t kmin_rb = LLONG_MAX, kmax_rb = -1;
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    const int flat = rb * ROWS + r;
+    valid[r] = flat < p.rows_total;
+    trow[r] = valid[r] ? flat / p.G : 0;
+    hrow[r] = kvh * p.G + (valid[r] ? flat % p.G : 0);
+    visible_range(base + trow[r], p.window, p.max_len, kmin[r], kmax[r]);
+    if (!valid[r]) {
+      kmin[r] = LLONG_MAX;
+      kmax[r] = -1;
+    }
+    kmin_rb = kmin[r] < kmin_rb ? kmin[r] : kmin_rb;
+    kmax_rb = kmax[r] > kmax_rb ? kmax[r] : kmax_rb;
+  }
+  const int64_t c0 = (int64_t)c * p.chunk;
+  if (c0 > kmax_rb || c0 + p.chunk - 1 < kmin_rb) return;  // block-uniform
+
+  float q[ROWS][VEC];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    if (valid[r]) {
+      load_q_row<T, D, VEC, LPR>(p, b, hrow[r], trow[r], li, q[r]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) q[r][e] = 0.0f;
+    }
+  }
+
+  float m[ROWS], l[ROWS], o[ROWS][VEC];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    m[r] = kNegInf;
+    l[r] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o[r][e] = 0.0f;
+  }
+
+  const T* kbase = static_cast<const T*>(p.kc) + b * p.skb + kvh * p.skh + li * VEC;
+  const T* vbase = static_cast<const T*>(p.vc) + b * p.skb + kvh * p.skh + li * VEC;
+  const int iters = p.chunk / KPI;
+  for (int it = 0; it < iters; ++it) {
+    const int64_t kb0 = c0 + (int64_t)it * KPI;
+    if (kb0 > kmax_rb || kb0 + KPI - 1 < kmin_rb) continue;  // block-uniform
+    const int64_t kg0 = kb0 + g * NK;
+    uint4 kraw[NK], vraw[NK];
+#pragma unroll
+    for (int u = 0; u < NK; ++u) {
+      const int64_t kp = kg0 + u;
+      if (kp >= kmin_rb && kp <= kmax_rb) {
+        kraw[u] = load16(kbase + kp * p.sks);
+        vraw[u] = load16(vbase + kp * p.sks);
+      } else {
+        kraw[u] = make_uint4(0, 0, 0, 0);
+        vraw[u] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    float kf[NK][VEC];
+#pragma unroll
+    for (int u = 0; u < NK; ++u) unpack16<T>(kraw[u], kf[u]);
+
+    float s[ROWS][NK];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+#pragma unroll
+      for (int u = 0; u < NK; ++u) {
+        float d = 0.0f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) d += q[r][e] * kf[u][e];
+        s[r][u] = group_sum<LPR>(d) * p.scale_log2;
+        const int64_t kp = kg0 + u;
+        if (kp < kmin[r] || kp > kmax[r]) s[r][u] = kNegInf;
+      }
+    }
+
+    float vf[NK][VEC];
+#pragma unroll
+    for (int u = 0; u < NK; ++u) unpack16<T>(vraw[u], vf[u]);
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      float mx = s[r][0];
+#pragma unroll
+      for (int u = 1; u < NK; ++u) mx = fmaxf(mx, s[r][u]);
+      const float m_new = fmaxf(m[r], mx);
+      const float alpha = rescale(m[r], m_new);
+      float pu[NK];
+      float psum = 0.0f;
+#pragma unroll
+      for (int u = 0; u < NK; ++u) {
+        pu[u] = exp2_masked(s[r][u], m_new);
+        psum += pu[u];
+      }
+      l[r] = l[r] * alpha + psum;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        float acc = o[r][e] * alpha;
+#pragma unroll
+        for (int u = 0; u < NK; ++u) acc += pu[u] * vf[u][e];
+        o[r][e] = acc;
+      }
+      m[r] = m_new;
+    }
+  }
+
+  // Merge the GPW groups of this wave: butterfly over lane distances LPR .. 32.
+#pragma unroll
+  for (int dist = LPR; dist < kWave; dist <<= 1) {
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      const float m_o = __shfl_xor(m[r], dist, kWave);
+      const float l_o = __shfl_xor(l[r], dist, kWave);
+      const float m_n = fmaxf(m[r], m_o);
+      const float a_s = rescale(m[r], m_n);
+      const float a_o = rescale(m_o, m_n);
+      l[r] = l[r] * a_s + l_o * a_o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float o_o = __shfl_xor(o[r][e], dist, kWave);
+        o[r][e] = o[r][e] * a_s + o_o * a_o;
+      }
+      m[r] = m_n;
+    }
+  }
+  (void)GPW;
+  if (tid % kWave < LPR) {
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sh_o[wave][r][li * VEC + e] = o[r][e];
+      if (li == 0) {
+        sh_m[wave][r] = m[r];
+        sh_l[wave][r] = l[r];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Merge the waves in order 0..3 and write the row's result for this chunk.
+  for (int idx = tid; idx < ROWS * D; idx += kSplitThreads) {
+    const int r = idx / D;
+    const int e = idx % D;
+    if (r >= ROWS) break;
+    const int flat = rb * ROWS + r;
+    if (flat >= p.rows_total) continue;
+    const int t = flat / p.G;
+    const int h = kvh * p.G + flat % p.G;
+    int64_t rkmin, rkmax;
+    visible_range(base + t, p.window, p.max_len, rkmin, rkmax);
+    if (c0 > rkmax || c0 + p.chunk - 1 < rkmin) continue;  // this chunk is outside the row
+    float M = sh_m[0][r];
+#pragma unroll
+    for (int w = 1; w < NWAVES; ++w) M = fmaxf(M, sh_m[w][r]);
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NWAVES; ++w) {
+      const float a = rescale(sh_m[w][r], M);
+      L = L + a * sh_l[w][r];
+      O = O + a * sh_o[w][r][e];
+    }
+    const int64_t cmin = rkmin / p.chunk;
+    const int64_t cmax = rkmax / p.chunk;
+    if (cmin == cmax) {
+      T* dst = static_cast<T*>(p.out) + b * p.sob + t * p.sot + h * p.soh;
+      dst[e] = from_f32<T>(O / L);
+    } else {
+      const int64_t rowid = ((int64_t)b * p.H + h) * p.T + t;
+      const int64_t slot = rowid * p.max_chunks + c;
+      p.ws_o[slot * D + e] = O;
+      if (e == 0) p.ws_ml[slot] = make_float2(M, L);
+    }
+  }
+}
+
+// One wave per (b, h, t) row: merges the row's chunk partials in chunk order.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void combine_kernel(SplitParams p) {
+  constexpr int EPL = D >= kWave ? D / kWave : 1;  // elements per lane
+  const int lane = threadIdx.x % kWave;
+  const int64_t row = (int64_t)blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  if (row >= (int64_t)p.B * p.H * p.T) return;
+  const int t = (int)(row % p.T);
+  const int h = (int)((row / p.T) % p.H);
+  const int b = (int)(row / ((int64_t)p.T * p.H));
+  const int64_t base = row_base(p.row_pos, p.pos_dev, p.pos0, b);
+  int64_t kmin, kmax;
+  visible_range(base + t, p.window, p.max_len, kmin, kmax);
+  if (kmax < kmin) return;
+  const int64_t cmin = kmin / p.chunk;
+  int64_t cmax = kmax / p.chunk;
+  if (cmax > p.max_chunks - 1) cmax = p.max_chunks - 1;
+  if (cmin >= cmax) return;  // single chunk: the split kernel wrote the output
+  const int64_t slot0 = row * p.max_chunks;  // row == (b*H + h)*T + t
+
+  float M = kNegInf;
+  for (int64_t c = cmin + lane; c <= cmax; c += kWave) M = fmaxf(M, p.ws_ml[slot0 + c].x);
+  M = group_max<kWave>(M);
+
+  float L = 0.0f, O[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) O[i] = 0.0f;
+  const bool active = lane * EPL < D;
+  for (int64_t c = cmin; c <= cmax; ++c) {
+    const float2 ml = p.ws_ml[slot0 + c];
+    const float a = rescale(ml.x, M);
+    L = L + a * ml.y;
+    if (active) {
+      const float* src = p.ws_o + (slot0 + c) * D + lane * EPL;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) O[i] = O[i] + a * src[i];
+    }
+  }
+  if (!active) return;
+  T* dst = static_cast<T*>(p.out) + b * p.sob + t * p.sot + h * p.soh + lane * EPL;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) dst[i] = from_f32<T>(O[i] / L);
+}
+
+// ---------------------------------------------------------------- host side
+static int vec_of(int dtype) { return dtype == FORGE_F32 ? 4 : 8; }
+
+static int rows_per_block(int rows_total) {
+  if (rows_total >= 8) return 8;
+  int r = 1;
+  while (r < rows_total) r <<= 1;
+  return r;
+}
+
+static int keys_per_iter(int dtype, int D) { return (kSplitThreads / (D / vec_of(dtype))) * kSplitNK; }
+
+static bool head_dim_ok(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
+
+static int auto_chunk(int dtype, int B, int T, int H, int K, int D, int64_t max_kv_len) {
+  const int G = H / K;
+  const int rows = rows_per_block(G * T);
+  const int64_t n_rb = (G * T + rows - 1) / rows;
+  const int64_t pairs = (int64_t)B * K * n_rb;
+  int chunk = keys_per_iter(dtype, D);
+  const int64_t len = max_kv_len > 0 ? max_kv_len : 1;
+  while (chunk * 2 <= kMaxChunk && pairs * ((len + chunk * 2 - 1) / (chunk * 2)) >= 2048) chunk *= 2;
+  return chunk;
+}
+
+template <typename T, int D>
+static int launch_split_d(const SplitParams& p, int rows, dim3 grid, hipStream_t s) {
+  switch (rows) {
+#define FORGE_ROWS(R) \
+  case R: hipLaunchKernelGGL((splitk_kernel<T, D, R>), grid, dim3(kSplitThreads), 0, s, p); break;
+    FORGE_ROWS(1) FORGE_ROWS(2) FORGE_ROWS(4) FORGE_ROWS(8)
+#undef FORGE_ROWS
+    default: return set_error("internal: rows per block");
+  }
+  int st = check_launch();
+  if (st || p.max_chunks < 2) return st;
+  const int64_t nrows = (int64_t)p.B * p.H * p.T;
+  const dim3 cgrid((unsigned)((nrows + 3) / 4));
+  hipLaunchKernelGGL((combine_kernel<T, D>), cgrid, dim3(256), 0, s, p);
+  return check_launch();
+}
+
+template <typename T>
+static int launch_split(const SplitParams& p, int D, int rows, dim3 grid, hipStream_t s) {
+  switch (D) {
+    case 32: return launch_split_d<T, 32>(p, rows, grid, s);
+    case 64: return launch_split_d<T, 64>(p, rows, grid, s);
+    case 128: return launch_split_d<T, 128>(p, rows, grid, s);
+    case 256: return launch_split_d<T, 256>(p, rows, grid, s);
+    default: return set_error("forge_attn_decode: head dim must be 32, 64, 128 or 256");
+  }
+}
+
+}  // namespace forge
+
+using namespace forge;
+
+extern "C" int forge_attn_decode_chunk(int dtype, int B, int T, int H, int K, int D,
+                                       int64_t max_kv_len) {
+  if (K <= 0 || H % K || !head_dim_ok(D) || T <= 0) return 0;
+  return auto_chunk(dtype, B, T, H, K, D, max_kv_len);
+}
+
+extern "C" size_t forge_attn_decode_workspace_bytes(int dtype, int B, int T, int H, int K,
+                                                    int D, int64_t max_kv_len, int chunk) {
+  (void)K;
+  if (chunk <= 0) chunk = (K > 0 && H % K == 0) ? auto_chunk(dtype, B, T, H, K, D, max_kv_len) : 64;
+  const int64_t max_chunks = (max_kv_len + chunk - 1) / chunk;
+  if (max_chunks < 2) return 0;
+  const int64_t slots = (int64_t)B * H * T * max_chunks;
+  const size_t ml = ((size_t)slots * sizeof(float2) + 255) / 256 * 256;
+  return ml + (size_t)slots * D * sizeof(float);
+}
+
+extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, const void* q,
+                                 int64_t sqb, int64_t sqh, int64_t sqt, const float* q_weight,
+                                 float eps, int flags, const float* cos, const float* sin,
+                                 int64_t s_cos_b, int64_t s_cos_t, const void* k_cache,
+                                 const void* v_cache, int64_t skb, int64_t skh, int64_t sks,
+                                 int64_t max_len, const int32_t* row_pos, const int64_t* pos_dev,
+                                 int64_t pos0, int64_t max_kv_len, int window, float scale,
+                                 int chunk, void* out, int64_t sob, int64_t sot, int64_t soh,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (dtype != FORGE_F32 && dtype != FORGE_BF16 && dtype != FORGE_F16)
+    return set_error("unknown dtype code");
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0) return set_error("sizes must be positive");
+  if (H % K) return set_error("n_heads must be a multiple of the KV heads");
+  if (!head_dim_ok(D)) return set_error("forge_attn_decode: head dim must be 32, 64, 128 or 256");
+  if (!q || !k_cache || !v_cache || !out) return set_error("null tensor pointer");
+  if ((flags & FORGE_ROPE) && (!cos || !sin)) return set_error("FORGE_ROPE needs cos and sin");
+  if (max_len <= 0) return set_error("cache length must be positive");
+  if (max_kv_len <= 0 || max_kv_len > max_len) max_kv_len = max_len;
+  if (!row_pos && !pos_dev && (pos0 < 0 || pos0 + T > max_len))
+    return set_error("KV cache full: pos + T exceeds the cache length");
+  if (!row_pos && !pos_dev && pos0 + T > max_kv_len) max_kv_len = pos0 + T;
+  if (window < 0) return set_error("window must be >= 0");
+  const int kpi = keys_per_iter(dtype, D);
+  if (chunk <= 0) chunk = auto_chunk(dtype, B, T, H, K, D, max_kv_len);
+  if (chunk % kpi) return set_error("chunk must be a multiple of the keys per block iteration");
+
+  SplitParams p{};
+  p.q = q;
+  p.sqb = sqb;
+  p.sqh = sqh;
+  p.sqt = sqt;
+  p.qw = q_weight;
+  p.eps = eps;
+  p.flags = flags;
+  p.cos = cos;
+  p.sin = sin;
+  p.csb = s_cos_b;
+  p.cst = s_cos_t;
+  p.kc = k_cache;
+  p.vc = v_cache;
+  p.skb = skb;
+  p.skh = skh;
+  p.sks = sks;
+  p.max_len = max_len;
+  p.row_pos = row_pos;
+  p.pos_dev = pos_dev;
+  p.pos0 = pos0;
+  p.B = B;
+  p.T = T;
+  p.H = H;
+  p.K = K;
+  p.G = H / K;
+  p.rows_total = p.G * T;
+  p.window = window;
+  p.scale_log2 = scale * kLog2e;
+  p.chunk = chunk;
+  p.max_chunks = (int)((max_kv_len + chunk - 1) / chunk);
+  p.out = out;
+  p.sob = sob;
+  p.sot = sot;
+  p.soh = soh;
+  if (p.max_chunks > 1) {
+    const size_t need = forge_attn_decode_workspace_bytes(dtype, B, T, H, K, D, max_kv_len, chunk);
+    if (!workspace || workspace_bytes < need) return set_error("workspace too small");
+    const int64_t slots = (int64_t)B * H * T * p.max_chunks;
+    const size_t ml = ((size_t)slots * sizeof(float2) + 255) / 256 * 256;
+    p.ws_ml = static_cast<float2*>(workspace);
+    p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + ml);
+  }
+  const int rows = rows_per_block(p.rows_total);
+  const int n_rb = (p.rows_total + rows - 1) / rows;
+  if ((int64_t)K * n_rb > 65535 || B > 65535) return set_error("grid too large");
+  const dim3 grid((unsigned)p.max_chunks, (unsigned)(K * n_rb), (unsigned)B);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case FORGE_F32: return launch_split<float>(p, D, rows, grid, s);
+    case FORGE_BF16: return launch_split<bf16>(p, D, rows, grid, s);
+    default: return launch_split<f16>(p, D, rows, grid, s);
+  }
+}

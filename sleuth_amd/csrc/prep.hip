@@ -1,0 +1,235 @@
+// Per-row head RMSNorm + NEOX RoPE, and the K/V cache append.
+//
+// One group of GW lanes owns one (b, head, t) row of D values. Lane i holds the VEC
+// values starting at i*VEC of the first half and the VEC values at D/2 + i*VEC of the
+// second half, so the RoPE pair (c, c + D/2) (rope.py:41-55) is in one lane and only
+// the RMS sum needs a cross-lane reduction. Math is fp32 with a single rounding to the
+// output dtype, as fused_ops._head_kernel (fused_ops.py:53-85).
+#include "common.h"
+#include "forge_internal.h"
+
+namespace forge {
+
+struct RowTensor {
+  const void* src;
+  int64_t sb, sh, st;
+  void* dst;
+  int64_t db, dh, dt;
+  const float* w;  // gain or nullptr
+  int heads;
+  int norm;
+  int rope;
+  int at_pos;  // 0: dst row t; 1: dst row base_b + t (cache write)
+};
+
+struct RowParams {
+  RowTensor t[2];
+  int ntensors;
+  int B, T, D;
+  float eps;
+  const float* cos;
+  const float* sin;
+  int64_t csb, cst;
+  const int32_t* row_pos;
+  const int64_t* pos_dev;
+  int64_t pos0;
+  int64_t dst_len;
+};
+
+template <typename T, int VEC>
+__device__ __forceinline__ void load_vec(const T* p, float* out) {
+  if constexpr (VEC * sizeof(T) == 16) {
+    unpack16<T>(load16(p), out);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) out[i] = to_f32<T>(p[i]);
+  }
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void store_vec(T* p, const float* in) {
+  if constexpr (VEC * sizeof(T) == 16) {
+    store16(p, pack16<T>(in));
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) p[i] = from_f32<T>(in[i]);
+  }
+}
+
+template <typename T, int VEC, int GW>
+__global__ __launch_bounds__(256) void row_norm_rope_kernel(RowParams p) {
+  constexpr int ROWS_PER_BLOCK = 256 / GW;
+  const int li = threadIdx.x % GW;
+  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + threadIdx.x / GW;
+  const int64_t rows0 = (int64_t)p.B * p.t[0].heads * p.T;
+  const int64_t rows1 = p.ntensors > 1 ? (int64_t)p.B * p.t[1].heads * p.T : 0;
+  if (row >= rows0 + rows1) return;  // whole group leaves together
+  const bool second = row >= rows0;
+  const RowTensor& rt = second ? p.t[1] : p.t[0];
+  const int64_t r = second ? row - rows0 : row;
+  const int t = (int)(r % p.T);
+  const int h = (int)((r / p.T) % rt.heads);
+  const int b = (int)(r / ((int64_t)p.T * rt.heads));
+
+  const int half = p.D / 2;
+  const int c0 = li * VEC;
+  const bool active = c0 < half;
+
+  int64_t drow = t;
+  if (rt.at_pos) {
+    drow = row_base(p.row_pos, p.pos_dev, p.pos0, b) + t;
+    if (drow < 0 || drow >= p.dst_len) return;  // never write past the cache
+  }
+
+  const T* src = static_cast<const T*>(rt.src) + b * rt.sb + h * rt.sh + t * rt.st;
+  float a[VEC], z[VEC];
+  if (active) {
+    load_vec<T, VEC>(src + c0, a);
+    load_vec<T, VEC>(src + half + c0, z);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) a[i] = z[i] = 0.0f;
+  }
+  if (rt.norm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) ss += a[i] * a[i] + z[i] * z[i];
+    ss = group_sum<GW>(ss);
+    const float rs = rsqrtf(ss / (float)p.D + p.eps);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      a[i] *= rs;
+      z[i] *= rs;
+    }
+    if (rt.w && active) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        a[i] *= rt.w[c0 + i];
+        z[i] *= rt.w[half + c0 + i];
+      }
+    }
+  }
+  if (!active) return;
+  if (rt.rope) {
+    const float* cr = p.cos + b * p.csb + t * p.cst;
+    const float* sr = p.sin + b * p.csb + t * p.cst;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const float na = a[i] * cr[c0 + i] - z[i] * sr[c0 + i];
+      const float nz = z[i] * cr[half + c0 + i] + a[i] * sr[half + c0 + i];
+      a[i] = na;
+      z[i] = nz;
+    }
+  }
+  T* dst = static_cast<T*>(rt.dst) + b * rt.db + h * rt.dh + drow * rt.dt;
+  store_vec<T, VEC>(dst + c0, a);
+  store_vec<T, VEC>(dst + half + c0, z);
+}
+
+template <typename T, int VEC>
+static int launch_rows_vec(const RowParams& p, int gw, hipStream_t s) {
+  const int64_t rows =
+      (int64_t)p.B * p.T * (p.t[0].heads + (p.ntensors > 1 ? p.t[1].heads : 0));
+  if (rows == 0) return 0;
+  const int64_t rpb = 256 / gw;
+  const dim3 grid((unsigned)((rows + rpb - 1) / rpb));
+  switch (gw) {
+#define FORGE_GW(W) \
+  case W: hipLaunchKernelGGL((row_norm_rope_kernel<T, VEC, W>), grid, dim3(256), 0, s, p); break;
+    FORGE_GW(1) FORGE_GW(2) FORGE_GW(4) FORGE_GW(8) FORGE_GW(16) FORGE_GW(32) FORGE_GW(64)
+#undef FORGE_GW
+    default: return set_error("row kernel: unsupported group width");
+  }
+  return check_launch();
+}
+
+template <typename T>
+static int launch_rows(const RowParams& p, hipStream_t s) {
+  const int half = p.D / 2;
+  constexpr int V16 = 16 / sizeof(T);
+  int vec = 1;
+  if (half % V16 == 0) vec = V16;
+  else if (half % 2 == 0) vec = 2;
+  const int lanes = (half + vec - 1) / vec;
+  int gw = 1;
+  while (gw < lanes) gw <<= 1;
+  if (gw > 64) return set_error("head dim too large for the row kernel (max 64 lanes per row)");
+  if (vec == V16) return launch_rows_vec<T, V16>(p, gw, s);
+  if (vec == 2) return launch_rows_vec<T, 2>(p, gw, s);
+  return launch_rows_vec<T, 1>(p, gw, s);
+}
+
+static int dispatch_rows(int dtype, const RowParams& p, hipStream_t s) {
+  switch (dtype) {
+    case FORGE_F32: return launch_rows<float>(p, s);
+    case FORGE_BF16: return launch_rows<bf16>(p, s);
+    case FORGE_F16: return launch_rows<f16>(p, s);
+    default: return set_error("unknown dtype code");
+  }
+}
+
+}  // namespace forge
+
+using namespace forge;
+
+extern "C" int forge_head_norm_rope(int dtype, const void* x, void* y, int B, int H, int T,
+                                    int D, int64_t sxb, int64_t sxh, int64_t sxt, int64_t syb,
+                                    int64_t syh, int64_t syt, const float* weight, float eps,
+                                    int norm, const float* cos, const float* sin,
+                                    int64_t s_cos_b, int64_t s_cos_t, void* stream) {
+  clear_error();
+  if (B < 0 || H < 0 || T < 0) return set_error("negative size");
+  if (D <= 0 || D % 2) return set_error("head dim must be even and positive");
+  if (!x || !y) return set_error("null tensor pointer");
+  if ((cos == nullptr) != (sin == nullptr)) return set_error("cos and sin must both be given");
+  RowParams p{};
+  p.t[0] = RowTensor{x, sxb, sxh, sxt, y, syb, syh, syt, weight, H, norm ? 1 : 0,
+                     cos ? 1 : 0, 0};
+  p.ntensors = 1;
+  p.B = B;
+  p.T = T;
+  p.D = D;
+  p.eps = eps;
+  p.cos = cos;
+  p.sin = sin;
+  p.csb = s_cos_b;
+  p.cst = s_cos_t;
+  return dispatch_rows(dtype, p, (hipStream_t)stream);
+}
+
+extern "C" int forge_kv_append(int dtype, int B, int T, int K, int D, const void* k,
+                               int64_t skb, int64_t skh, int64_t skt, const void* v,
+                               int64_t svb, int64_t svh, int64_t svt, void* k_dst, void* v_dst,
+                               int64_t sdb, int64_t sdh, int64_t sds, int64_t dst_len,
+                               const int32_t* row_pos, const int64_t* pos_dev, int64_t pos0,
+                               const float* k_weight, float eps, int flags, const float* cos,
+                               const float* sin, int64_t s_cos_b, int64_t s_cos_t,
+                               void* stream) {
+  clear_error();
+  if (B < 0 || K <= 0 || T < 0) return set_error("bad sizes");
+  if (D <= 0 || D % 2) return set_error("head dim must be even and positive");
+  if (!k || !v || !k_dst || !v_dst) return set_error("null tensor pointer");
+  const bool rope = flags & FORGE_ROPE;
+  if (rope && (!cos || !sin)) return set_error("FORGE_ROPE needs cos and sin");
+  if (!row_pos && !pos_dev && (pos0 < 0 || pos0 + T > dst_len))
+    return set_error("KV cache full: pos + T exceeds the cache length");
+  RowParams p{};
+  p.t[0] = RowTensor{k, skb, skh, skt, k_dst, sdb, sdh, sds, k_weight, K,
+                     (flags & FORGE_NORM_QK) ? 1 : 0, rope ? 1 : 0, 1};
+  p.t[1] = RowTensor{v, svb, svh, svt, v_dst, sdb, sdh, sds, nullptr, K,
+                     (flags & FORGE_NORM_V) ? 1 : 0, 0, 1};
+  p.ntensors = 2;
+  p.B = B;
+  p.T = T;
+  p.D = D;
+  p.eps = eps;
+  p.cos = cos;
+  p.sin = sin;
+  p.csb = s_cos_b;
+  p.cst = s_cos_t;
+  p.row_pos = row_pos;
+  p.pos_dev = pos_dev;
+  p.pos0 = pos0;
+  p.dst_len = dst_len;
+  return dispatch_rows(dtype, p, (hipStream_t)stream);
+}

@@ -1,0 +1,256 @@
+"""Torch-tensor front ends of the HIP kernels (C ABI in include/forge_attn.h).
+
+These functions only check shapes on the host, pick pointers/strides and launch on
+torch's current stream. They never compute anything themselves: if the library is not
+built they raise (sleuth_amd._lib.ForgeError).
+
+Layouts (reference names): q [B,H,T,D] (any strides, last dim contiguous: the transposed
+q_proj view, attention.py:106), k/v [B,K,T,D], caches [B,K,max_len,D] (kv_cache.py:31),
+outputs [B,T,H,D] (attention.py:155).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import BF16, F16, F32, NORM_QK, NORM_V, ROPE, check, lib
+
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype} (float32, bfloat16, float16)") from None
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _need_device(*ts: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError("forge kernels need tensors on the GPU")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError("all tensors must be on the same GPU")
+    assert dev is not None
+    return dev
+
+
+def _last_dim_contiguous(t: torch.Tensor, name: str) -> None:
+    if t.stride(-1) != 1:
+        raise ValueError(f"{name}: the last dimension must be contiguous")
+
+
+def _weight(w: torch.Tensor | None, D: int) -> torch.Tensor | None:
+    if w is None:
+        return None
+    if w.numel() != D:
+        raise ValueError(f"norm gain has {w.numel()} values for head dim {D}")
+    return w.detach().to(torch.float32).contiguous()
+
+
+def _rope_tables(cos, sin, B: int, T: int, D: int):
+    """cos/sin [T, D] (shared positions) or [B, T, D] (per row) fp32 -> (cos, sin, s_b, s_t)."""
+    if cos is None and sin is None:
+        return None, None, 0, 0
+    if cos is None or sin is None:
+        raise ValueError("cos and sin must both be given")
+    if cos.shape != sin.shape or cos.shape[-1] != D or cos.shape[-2] != T or cos.dim() not in (2, 3):
+        raise ValueError(f"cos/sin must be [T, D] or [B, T, D] with T={T}, D={D}; got {tuple(cos.shape)}")
+    if cos.dim() == 3 and cos.shape[0] not in (1, B):
+        raise ValueError("per-row cos/sin need batch size B")
+    cos = cos.to(torch.float32)
+    sin = sin.to(torch.float32)
+    if cos.stride(-1) != 1:
+        cos = cos.contiguous()
+    if sin.stride() != cos.stride():
+        sin = sin.contiguous()
+        cos = cos.contiguous()
+    s_b = cos.stride(0) if cos.dim() == 3 and cos.shape[0] == B and B > 1 else 0
+    return cos, sin, s_b, cos.stride(-2)
+
+
+def _positions(pos, pos_dev, row_pos, B: int, device):
+    """(row_pos int32 [B] | None, pos_dev int64 [1] | None, pos0 int)."""
+    if row_pos is not None:
+        if row_pos.dtype != torch.int32 or row_pos.numel() != B or row_pos.device != device:
+            raise ValueError("row_pos must be an int32 [B] tensor on the GPU")
+        return row_pos.contiguous(), None, 0
+    if pos_dev is not None:
+        if pos_dev.dtype != torch.int64 or pos_dev.device != device:
+            raise ValueError("pos_dev must be an int64 tensor on the GPU")
+        return None, pos_dev, 0
+    return None, None, int(pos or 0)
+
+
+def head_norm_rope(x: torch.Tensor, weight: torch.Tensor | None = None, eps: float = 1e-6,
+                   cos: torch.Tensor | None = None, sin: torch.Tensor | None = None,
+                   norm: bool = True) -> torch.Tensor:
+    """fused_ops.head_norm_rope (fused_ops.py:101-121): x [B,H,T,D] -> per-head RMSNorm
+    (gain `weight`, if norm) then NEOX RoPE (if cos/sin), one rounding; same layout as x."""
+    B, H, T, D = x.shape
+    dev = _need_device(x, cos, sin)
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    y = torch.empty_like(x)
+    c, s, s_b, s_t = _rope_tables(cos, sin, B, T, D)
+    w = _weight(weight, D)
+    st = lib().forge_head_norm_rope(dtype_code(x), _ptr(x), _ptr(y), B, H, T, D,
+                                    x.stride(0), x.stride(1), x.stride(2),
+                                    y.stride(0), y.stride(1), y.stride(2),
+                                    _ptr(w), float(eps), int(bool(norm)),
+                                    _ptr(c), _ptr(s), s_b, s_t, _stream(dev))
+    check(st, "forge_head_norm_rope")
+    return y
+
+
+def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *,
+              pos: int | None = None, pos_dev: torch.Tensor | None = None,
+              row_pos: torch.Tensor | None = None, k_weight: torch.Tensor | None = None,
+              eps: float = 1e-6, norm_k: bool = False, norm_v: bool = False,
+              cos: torch.Tensor | None = None, sin: torch.Tensor | None = None) -> None:
+    """Normalise/rotate the new k (and v_norm v) and write them into the cache at
+    base_b + t (KVCache.update, kv_cache.py:52-60; StaticKVCache.update 107-114)."""
+    B, K, T, D = k.shape
+    if v.shape != k.shape:
+        raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+    if k_cache.shape != v_cache.shape or k_cache.dim() != 4 or k_cache.shape[0] != B or \
+            k_cache.shape[1] != K or k_cache.shape[3] != D:
+        raise ValueError(f"cache {tuple(k_cache.shape)} does not fit new k {tuple(k.shape)}")
+    if k_cache.stride() != v_cache.stride():
+        raise ValueError("k and v caches must have the same strides")
+    if k.dtype != k_cache.dtype or v.dtype != k_cache.dtype:
+        k, v = k.to(k_cache.dtype), v.to(k_cache.dtype)
+    dev = _need_device(k, v, k_cache, v_cache, cos, sin)
+    for t, n in ((k, "k"), (v, "v"), (k_cache, "k_cache")):
+        _last_dim_contiguous(t, n)
+    rp, pd, p0 = _positions(pos, pos_dev, row_pos, B, dev)
+    c, s, s_b, s_t = _rope_tables(cos, sin, B, T, D)
+    flags = (NORM_QK if norm_k else 0) | (ROPE if c is not None else 0) | (NORM_V if norm_v else 0)
+    w = _weight(k_weight, D) if norm_k else None
+    st = lib().forge_kv_append(dtype_code(k_cache), B, T, K, D,
+                               _ptr(k), k.stride(0), k.stride(1), k.stride(2),
+                               _ptr(v), v.stride(0), v.stride(1), v.stride(2),
+                               _ptr(k_cache), _ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
+                               k_cache.stride(2), k_cache.shape[2], _ptr(rp), _ptr(pd), p0,
+                               _ptr(w), float(eps), flags, _ptr(c), _ptr(s), s_b, s_t, _stream(dev))
+    check(st, "forge_kv_append")
+
+
+def decode_chunk(dtype: torch.dtype, B: int, T: int, H: int, K: int, D: int, max_kv_len: int) -> int:
+    return lib().forge_attn_decode_chunk(_DTYPES[dtype], B, T, H, K, D, int(max_kv_len))
+
+
+def decode_workspace_bytes(dtype: torch.dtype, B: int, T: int, H: int, K: int, D: int,
+                           max_kv_len: int, chunk: int = 0) -> int:
+    return lib().forge_attn_decode_workspace_bytes(_DTYPES[dtype], B, T, H, K, D, int(max_kv_len), int(chunk))
+
+
+def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *, scale: float,
+                pos: int | None = None, pos_dev: torch.Tensor | None = None,
+                row_pos: torch.Tensor | None = None, max_kv_len: int | None = None,
+                window: int = 0, q_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                norm_q: bool = False, cos: torch.Tensor | None = None,
+                sin: torch.Tensor | None = None, chunk: int = 0, out: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Split-K attention of the T new queries q [B,H,T,D] against the cache, whose rows
+    hold base_b + T valid keys (the new ones included). Returns [B,T,H,D]."""
+    B, H, T, D = q.shape
+    Bc, K, max_len, Dc = k_cache.shape
+    if Bc != B or Dc != D or v_cache.shape != k_cache.shape or H % K:
+        raise ValueError(f"q {tuple(q.shape)} does not fit cache {tuple(k_cache.shape)}")
+    if k_cache.stride() != v_cache.stride():
+        raise ValueError("k and v caches must have the same strides")
+    if q.dtype != k_cache.dtype:
+        raise ValueError(f"q is {q.dtype} but the cache is {k_cache.dtype}")
+    dev = _need_device(q, k_cache, v_cache, cos, sin, out, workspace)
+    _last_dim_contiguous(q, "q")
+    _last_dim_contiguous(k_cache, "k_cache")
+    rp, pd, p0 = _positions(pos, pos_dev, row_pos, B, dev)
+    if max_kv_len is None:
+        max_kv_len = p0 + T if (rp is None and pd is None) else max_len
+    max_kv_len = max(1, min(int(max_kv_len), max_len))
+    c, s, s_b, s_t = _rope_tables(cos, sin, B, T, D)
+    flags = (NORM_QK if norm_q else 0) | (ROPE if c is not None else 0)
+    w = _weight(q_weight, D) if norm_q else None
+    if out is None:
+        out = torch.empty(B, T, H, D, dtype=q.dtype, device=dev)
+    elif out.shape != (B, T, H, D) or out.dtype != q.dtype:
+        raise ValueError(f"out must be [B,T,H,D] = {(B, T, H, D)} {q.dtype}")
+    dt = dtype_code(q)
+    if chunk <= 0:
+        chunk = lib().forge_attn_decode_chunk(dt, B, T, H, K, D, max_kv_len)
+    need = lib().forge_attn_decode_workspace_bytes(dt, B, T, H, K, D, max_kv_len, chunk)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    st = lib().forge_attn_decode(dt, B, T, H, K, D, _ptr(q), q.stride(0), q.stride(1), q.stride(2),
+                                 _ptr(w), float(eps), flags, _ptr(c), _ptr(s), s_b, s_t,
+                                 _ptr(k_cache), _ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
+                                 k_cache.stride(2), max_len, _ptr(rp), _ptr(pd), p0, max_kv_len,
+                                 int(window), float(scale), int(chunk),
+                                 _ptr(out), out.stride(0), out.stride(1), out.stride(2),
+                                 _ptr(workspace), ws_bytes, _stream(dev))
+    check(st, "forge_attn_decode")
+    return out
+
+
+PREFILL_HEAD_DIMS = (64, 128, 256)
+
+
+def prefill_supported(q: torch.Tensor) -> bool:
+    return q.dtype in (torch.bfloat16, torch.float16) and q.shape[-1] in PREFILL_HEAD_DIMS
+
+
+def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float, offset: int = 0,
+                 window: int = 0, q_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                 norm_q: bool = False, cos: torch.Tensor | None = None,
+                 sin: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal flash attention on MFMA: queries at positions offset..offset+T-1 over keys
+    0..offset+T-1 of k/v [B,K,>=offset+T,D]. Returns [B,T,H,D]."""
+    B, H, T, D = q.shape
+    Bk, K, S, Dk = k.shape
+    if Bk != B or Dk != D or v.shape != k.shape or H % K:
+        raise ValueError(f"q {tuple(q.shape)} does not fit k/v {tuple(k.shape)}")
+    if S < offset + T:
+        raise ValueError(f"k/v hold {S} positions, need offset + T = {offset + T}")
+    if k.stride() != v.stride():
+        raise ValueError("k and v must have the same strides")
+    if not prefill_supported(q) or k.dtype != q.dtype:
+        raise ValueError(f"MFMA prefill takes bf16/fp16 with head dim in {PREFILL_HEAD_DIMS}")
+    dev = _need_device(q, k, v, cos, sin, out)
+    _last_dim_contiguous(q, "q")
+    _last_dim_contiguous(k, "k")
+    c, s, s_b, s_t = _rope_tables(cos, sin, B, T, D)
+    if s_b:
+        raise ValueError("prefill takes [T, D] cos/sin shared by the batch")
+    flags = (NORM_QK if norm_q else 0) | (ROPE if c is not None else 0)
+    w = _weight(q_weight, D) if norm_q else None
+    if out is None:
+        out = torch.empty(B, T, H, D, dtype=q.dtype, device=dev)
+    elif out.shape != (B, T, H, D) or out.dtype != q.dtype:
+        raise ValueError(f"out must be [B,T,H,D] = {(B, T, H, D)} {q.dtype}")
+    st = lib().forge_attn_prefill(dtype_code(q), B, T, H, K, D, _ptr(q), q.stride(0), q.stride(1),
+                                  q.stride(2), _ptr(w), float(eps), flags, _ptr(c), _ptr(s), s_t,
+                                  _ptr(k), _ptr(v), k.stride(0), k.stride(1), k.stride(2),
+                                  int(offset), int(window), float(scale),
+                                  _ptr(out), out.stride(0), out.stride(1), out.stride(2), _stream(dev))
+    check(st, "forge_attn_prefill")
+    return out
+
+
+__all__ = ["head_norm_rope", "kv_append", "attn_decode", "attn_prefill", "decode_chunk",
+           "decode_workspace_bytes", "prefill_supported", "dtype_code", "_lib"]

@@ -1,0 +1,230 @@
+"""Parity of each HIP kernel, called through the C ABI (sleuth_amd.ops), with the CPU
+oracle on identical seeded inputs. Tolerances: fp32 max-abs <= 1e-4, bf16/fp16 <= 2e-2."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from conftest import gpu_available
+from helpers import gen, max_abs, qkv_proj_views, randn, scale_of, tables, tol
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
+
+DEV = "cuda"
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def ops():
+    from sleuth_amd import ops as o
+
+    return o
+
+
+# ------------------------------------------------------------------ head_norm_rope
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("D", [16, 32, 48, 64, 96, 128, 256])
+def test_head_norm_rope(dtype, D):
+    """fused_ops.head_norm_rope semantics (fused_ops.py:101-121), incl. the reference's
+    odd sizes (test_fused_ops.py:29-40) and stride preservation (test_fused_ops.py:37)."""
+    g = gen(D)
+    B, H, T = 2, 3, 7
+    q = randn(g, B, T, H, D, dtype=dtype).transpose(1, 2)       # [B,H,T,D] strided
+    w = (1 + 0.1 * randn(g, D)).to(dtype)
+    cos, sin = tables(D, 64, 1e4)
+    cos, sin = cos[10:10 + T], sin[10:10 + T]
+    ref = oracle.head_norm_rope(q, w, 1e-6, cos, sin)
+    got = ops().head_norm_rope(q.to(DEV), w.to(DEV), 1e-6, cos.to(DEV), sin.to(DEV))
+    assert got.shape == q.shape and got.stride() == q.stride()
+    assert max_abs(got, ref) <= (2e-6 if dtype == torch.float32 else tol(dtype))
+    # norm only / rope only
+    ref2 = oracle.head_norm_rope(q, None, 1e-6)
+    got2 = ops().head_norm_rope(q.to(DEV), None, 1e-6)
+    assert max_abs(got2, ref2) <= (2e-6 if dtype == torch.float32 else tol(dtype))
+    ref3 = oracle.head_norm_rope(q, None, 0.0, cos, sin, norm=False)
+    got3 = ops().head_norm_rope(q.to(DEV), None, 0.0, cos.to(DEV), sin.to(DEV), norm=False)
+    assert max_abs(got3, ref3) <= (2e-6 if dtype == torch.float32 else tol(dtype))
+
+
+def test_head_norm_rope_rows_independent():
+    """A row's result does not depend on how many rows run together (bitwise;
+    test_fused_ops.py:41-44)."""
+    g = gen(3)
+    x = randn(g, 4, 6, 9, 128, dtype=torch.bfloat16).to(DEV)
+    w = (1 + 0.1 * randn(g, 128)).to(DEV)
+    a = ops().head_norm_rope(x, w, 1e-6)[:1]
+    b = ops().head_norm_rope(x[:1].contiguous(), w, 1e-6)
+    assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------ kv_append
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("mode", ["pos", "row_pos", "pos_dev"])
+def test_kv_append(dtype, D, mode):
+    g = gen(D + len(mode))
+    B, K, T, L = 3, 2, 5, 40
+    _, k, v = qkv_proj_views(g, B, T, 4, K, D, dtype)
+    kw_ = (1 + 0.1 * randn(g, D)).to(dtype)
+    cos, sin = tables(D, L, 1e6)
+    base = [7, 7, 7] if mode != "row_pos" else [0, 13, 35]
+    cache_k = torch.full((B, K, L, D), 1e4, dtype=dtype)   # poison: must survive outside the write
+    cache_v = cache_k.clone()
+    kc, vc = cache_k.to(DEV), cache_v.to(DEV)
+    if mode == "row_pos":
+        c = torch.stack([cos[b:b + T] for b in base])
+        s = torch.stack([sin[b:b + T] for b in base])
+        ops().kv_append(k.to(DEV), v.to(DEV), kc, vc, row_pos=torch.tensor(base, dtype=torch.int32, device=DEV),
+                        k_weight=kw_.to(DEV), eps=1e-6, norm_k=True, norm_v=True, cos=c.to(DEV), sin=s.to(DEV))
+    else:
+        c, s = cos[7:7 + T], sin[7:7 + T]
+        kwargs = {"pos": 7} if mode == "pos" else {"pos_dev": torch.tensor([7], device=DEV)}
+        ops().kv_append(k.to(DEV), v.to(DEV), kc, vc, k_weight=kw_.to(DEV), eps=1e-6, norm_k=True,
+                        norm_v=True, cos=c.to(DEV), sin=s.to(DEV), **kwargs)
+    t = tol(dtype) if dtype != torch.float32 else 2e-6
+    for b in range(B):
+        p = base[b]
+        cb, sb = (c[b], s[b]) if mode == "row_pos" else (c, s)
+        ref_k = oracle.head_norm_rope(k[b:b + 1], kw_, 1e-6, cb, sb)
+        ref_v = oracle.head_norm_rope(v[b:b + 1], None, 1e-6)
+        assert max_abs(kc[b:b + 1, :, p:p + T].cpu(), ref_k) <= t
+        assert max_abs(vc[b:b + 1, :, p:p + T].cpu(), ref_v) <= t
+        keep = torch.ones(L, dtype=torch.bool)
+        keep[p:p + T] = False
+        poison = torch.tensor(1e4, dtype=dtype).item()
+        assert torch.all(kc[b, :, keep.to(DEV)].float() == poison)
+        assert torch.all(vc[b, :, keep.to(DEV)].float() == poison)
+
+
+def test_kv_append_full_cache_rejected():
+    k = torch.zeros(1, 1, 4, 64, device=DEV, dtype=torch.bfloat16)
+    c = torch.zeros(1, 1, 8, 64, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="KV cache full"):
+        ops().kv_append(k, k, c, c.clone(), pos=6)
+
+
+# ------------------------------------------------------------------ split-K decode / verify
+def _decode_case(seed, dtype, B, H, K, D, T, lens, window, theta=1e4, max_len=None, fuse=True, chunk=0):
+    """Cache rows filled with N(0,1) up to lens[b] (the new tokens' K/V included); raw q
+    normalised in the kernel (fuse) or beforehand. Returns (got [B,T,H,D], ref [B,T,H,D])."""
+    g = gen(seed)
+    max_len = max_len or max(lens) + 3
+    kc = randn(g, B, K, max_len, D, dtype=dtype)
+    vc = randn(g, B, K, max_len, D, dtype=dtype)
+    q = randn(g, B, T, H, D, dtype=dtype).transpose(1, 2)
+    w = (1 + 0.1 * randn(g, D)).to(dtype)
+    cos_t, sin_t = tables(D, max_len, theta)
+    base = [L - T for L in lens]
+    c = torch.stack([cos_t[p:p + T] for p in base])
+    s = torch.stack([sin_t[p:p + T] for p in base])
+    qn = oracle.head_norm_rope(q, w, 1e-6, c, s)
+    ref = oracle.ragged_decode(qn.float(), kc.float(), vc.float(), lens, window, scale_of(D))
+    row_pos = torch.tensor(base, dtype=torch.int32, device=DEV)
+    if fuse:
+        got = ops().attn_decode(q.to(DEV), kc.to(DEV), vc.to(DEV), scale=scale_of(D), row_pos=row_pos,
+                                max_kv_len=max(lens), window=window, q_weight=w.to(DEV), eps=1e-6,
+                                norm_q=True, cos=c.to(DEV), sin=s.to(DEV), chunk=chunk)
+    else:
+        got = ops().attn_decode(qn.to(DEV), kc.to(DEV), vc.to(DEV), scale=scale_of(D), row_pos=row_pos,
+                                max_kv_len=max(lens), window=window, chunk=chunk)
+    return got.cpu(), ref.transpose(1, 2)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("HK", [(8, 4), (12, 4), (16, 8), (8, 1), (4, 4)])
+def test_decode_single_token(dtype, D, HK):
+    H, K = HK
+    lens = [1, 17, 300, 777]
+    got, ref = _decode_case(100 + D + H, dtype, 4, H, K, D, 1, lens, 0)
+    assert max_abs(got, ref) <= tol(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T", [2, 4, 5, 16])
+@pytest.mark.parametrize("window", [0, 64])
+def test_verify_multi_token(dtype, T, window):
+    """k-token speculative verify (attention.py:192-193): causal among the new tokens."""
+    got, ref = _decode_case(7 + T + window, dtype, 3, 8, 1, 256 if dtype != torch.float32 else 128,
+                            T, [T, 200, 1100], window, theta=1e6)
+    assert max_abs(got, ref) <= tol(dtype)
+
+
+@pytest.mark.parametrize("window", [0, 5, 100])
+def test_fp32_prefill_through_splitk(window):
+    """Config-1 shape: fp32 causal prefill of 256 tokens on the general (split-K) path."""
+    got, ref = _decode_case(11, torch.float32, 1, 8, 4, 32, 256, [256], window)
+    assert max_abs(got, ref) <= 1e-4
+
+
+def test_decode_prenormalised_q():
+    got, ref = _decode_case(12, torch.bfloat16, 2, 16, 8, 128, 1, [4000, 4097], 0, fuse=False)
+    assert max_abs(got, ref) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_verify_rows_equal_single_decodes_bitwise(dtype):
+    """A verify row (T = 5) equals decoding that token alone, bit for bit (same chunk):
+    the property speculative decoding relies on (fused_ops.py:19-20)."""
+    g = gen(5)
+    B, H, K, D, T, L = 2, 8, 2, 128, 5, 1500
+    kc = randn(g, B, K, L + 8, D, dtype=dtype).to(DEV)
+    vc = randn(g, B, K, L + 8, D, dtype=dtype).to(DEV)
+    q = randn(g, B, H, T, D, dtype=dtype).to(DEV)
+    sc = scale_of(D)
+    for window in (0, 300):
+        allv = ops().attn_decode(q, kc, vc, scale=sc, pos=L - T, window=window, chunk=256)
+        for t in range(T):
+            one = ops().attn_decode(q[:, :, t:t + 1], kc, vc, scale=sc, pos=L - T + t, window=window, chunk=256)
+            assert torch.equal(allv[:, t:t + 1], one), (window, t)
+
+
+def test_decode_pos_dev_matches_host_pos():
+    g = gen(9)
+    B, H, K, D, T, L = 2, 16, 8, 128, 3, 900
+    kc = randn(g, B, K, 1024, D, dtype=torch.bfloat16).to(DEV)
+    vc = randn(g, B, K, 1024, D, dtype=torch.bfloat16).to(DEV)
+    q = randn(g, B, H, T, D, dtype=torch.bfloat16).to(DEV)
+    a = ops().attn_decode(q, kc, vc, scale=0.1, pos=L - T, chunk=128)
+    b = ops().attn_decode(q, kc, vc, scale=0.1, pos_dev=torch.tensor([L - T], device=DEV),
+                          max_kv_len=1024, chunk=128)
+    assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------ MFMA prefill
+def _prefill_case(seed, dtype, B, H, K, D, T, offset, window, theta=1e4):
+    g = gen(seed)
+    S = offset + T
+    q = randn(g, B, T, H, D, dtype=dtype).transpose(1, 2)
+    w = (1 + 0.1 * randn(g, D)).to(dtype)
+    kc = randn(g, B, K, S + 5, D, dtype=dtype)
+    vc = randn(g, B, K, S + 5, D, dtype=dtype)
+    cos_t, sin_t = tables(D, S, theta)
+    c, s = cos_t[offset:S], sin_t[offset:S]
+    qn = oracle.head_norm_rope(q, w, 1e-6, c, s)
+    ref = oracle.sdpa(qn.float(), kc[:, :, :S].float(), vc[:, :, :S].float(), offset, window, scale_of(D))
+    got = ops().attn_prefill(q.to(DEV), kc.to(DEV), vc.to(DEV), scale=scale_of(D), offset=offset,
+                             window=window, q_weight=w.to(DEV), eps=1e-6, norm_q=True,
+                             cos=c.to(DEV), sin=s.to(DEV))
+    return got.cpu(), ref.transpose(1, 2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("T,offset", [(128, 0), (300, 0), (200, 37), (65, 500)])
+def test_prefill(dtype, D, T, offset):
+    got, ref = _prefill_case(D + T + offset, dtype, 2, 4, 2, D, T, offset, 0)
+    assert max_abs(got, ref) <= tol(dtype)
+
+
+@pytest.mark.parametrize("window", [1, 64, 100, 1024])
+def test_prefill_sliding_window(window):
+    got, ref = _prefill_case(window, torch.bfloat16, 1, 8, 1, 128, 700, 40, window)
+    assert max_abs(got, ref) <= 2e-2
+
+
+def test_prefill_rejects_fp32():
+    q = torch.zeros(1, 2, 4, 128, device=DEV)
+    with pytest.raises(ValueError):
+        ops().attn_prefill(q, q[:, :1], q[:, :1], scale=1.0)
