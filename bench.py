@@ -1,0 +1,397 @@
+"""Benchmark of the FORGE attention hot path on one MI355X.
+
+Headline (BASELINE.json metric): decode attention of config C4 -- batch 64, Qwen3-0.6B
+heads (16 q / 8 kv, head dim 128, bf16), per-row KV lengths uniform in [1024, 32768]
+from a seed, one new token per row. A step is one layer's attention for the batch:
+the new K/V are normalised/rotated and appended to the cache (forge_kv_append), then
+split-K attention with the q norm + RoPE fused (forge_attn_decode). `value` is the
+step's algorithmic HBM bytes / step time (GB/s); tokens/s = 64 / (28 layers x step).
+Beside it: C3 causal prefill (4 x 4096 tokens, bf16) in TFLOP/s, each dominant kernel's
+roofline fraction, and the oracle (torch SDPA on the CPU) timed on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--extra]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, TFLOP/s
+N_LAYERS = 28                # Qwen3-0.6B: tokens/s counts 28 layers per token
+METRIC = "decode attn HBM GB/s + tokens/s (bs64, 32k ctx); prefill bf16 TFLOPS at 4k"
+
+
+# ----------------------------------------------------------------------------- inputs
+def c4_lengths(seed: int = 0, B: int = 64, lo: int = 1024, hi: int = 32768) -> list[int]:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, hi + 1, (B,), generator=g).tolist()
+
+
+class DecodeWorkload:
+    """One layer of a ragged decode batch: caches [B, K, max_len, D] filled with N(0,1)
+    up to each row's length, raw q/k/v of the new token, norm gains, RoPE rows."""
+
+    def __init__(self, lens, H, K, D, theta, dtype, dev, seed=0, T=1, window=0, n_layers=1):
+        self.lens, self.B, self.H, self.K, self.D, self.T = lens, len(lens), H, K, D, T
+        self.window, self.dtype, self.dev = window, dtype, dev
+        self.max_len = max(lens)
+        g = torch.Generator(device=dev).manual_seed(seed)
+        shape = (self.B, K, self.max_len, D)
+        self.k_caches = [torch.randn(shape, generator=g, device=dev, dtype=dtype) for _ in range(n_layers)]
+        self.v_caches = [torch.randn(shape, generator=g, device=dev, dtype=dtype) for _ in range(n_layers)]
+        B = self.B
+        self.q = torch.randn(B, T, H, D, generator=g, device=dev, dtype=dtype).transpose(1, 2)
+        self.k = torch.randn(B, T, K, D, generator=g, device=dev, dtype=dtype).transpose(1, 2)
+        self.v = torch.randn(B, T, K, D, generator=g, device=dev, dtype=dtype).transpose(1, 2)
+        # norm gains: bf16 parameters, held in fp32 by the caller (converted once, like the module)
+        self.wq = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(dtype).float()
+        self.wk = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(dtype).float()
+        import oracle  # RoPE tables only (the same fp32 formula the model buffers use)
+
+        cos, sin = oracle.rope_tables(D, self.max_len + T, theta)
+        base = torch.tensor([L - T for L in lens])
+        idx = base[:, None] + torch.arange(T)[None, :]
+        self.cos = cos[idx].to(dev)
+        self.sin = sin[idx].to(dev)
+        self.row_pos = base.to(torch.int32).to(dev)
+        self.scale = 1.0 / math.sqrt(D)
+        self.out = torch.empty(B, T, H, D, device=dev, dtype=dtype)
+        from sleuth_amd import ops
+
+        self.chunk = ops.decode_chunk(dtype, B, T, H, K, D, self.max_len)
+        nbytes = ops.decode_workspace_bytes(dtype, B, T, H, K, D, self.max_len, self.chunk)
+        self.ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        self.layer = 0
+
+    def append(self, layer=None):
+        from sleuth_amd import ops
+
+        i = self.layer if layer is None else layer
+        ops.kv_append(self.k, self.v, self.k_caches[i], self.v_caches[i], row_pos=self.row_pos,
+                      k_weight=self.wk, eps=1e-6, norm_k=True, cos=self.cos, sin=self.sin)
+
+    def attend(self, layer=None):
+        from sleuth_amd import ops
+
+        i = self.layer if layer is None else layer
+        return ops.attn_decode(self.q, self.k_caches[i], self.v_caches[i], scale=self.scale,
+                               row_pos=self.row_pos, max_kv_len=self.max_len, window=self.window,
+                               q_weight=self.wq, eps=1e-6, norm_q=True, cos=self.cos, sin=self.sin,
+                               chunk=self.chunk, out=self.out, workspace=self.ws)
+
+    def step(self):
+        self.append()
+        self.attend()
+        self.layer = (self.layer + 1) % len(self.k_caches)
+
+    def visible(self, L):
+        return min(L, self.window + self.T - 1) if self.window else L
+
+    def kv_bytes(self) -> int:
+        s = torch.finfo(self.dtype).bits // 8
+        return sum(2 * self.K * self.visible(L) * self.D * s for L in self.lens)
+
+    def step_bytes(self) -> int:
+        """Algorithmic bytes of one step: K/V of the positions each row reads, q read,
+        o written, new K/V written."""
+        s = torch.finfo(self.dtype).bits // 8
+        B, H, K, D, T = self.B, self.H, self.K, self.D, self.T
+        return self.kv_bytes() + 2 * B * H * T * D * s + 2 * B * K * T * D * s
+
+    def attend_bytes(self) -> int:
+        """Algorithmic bytes of the attention call: K/V reads + q read + o write."""
+        s = torch.finfo(self.dtype).bits // 8
+        return self.kv_bytes() + 2 * self.B * self.H * self.T * self.D * s
+
+
+class PrefillWorkload:
+    """C3 prefill: B x T causal, raw q/k/v, gains N(1, 0.1), RoPE theta 1e6."""
+
+    def __init__(self, B, T, H, K, D, theta, dtype, dev, seed=1):
+        self.B, self.T, self.H, self.K, self.D = B, T, H, K, D
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.q = torch.randn(B, T, H, D, generator=g, device=dev, dtype=dtype).transpose(1, 2)
+        self.k = torch.randn(B, T, K, D, generator=g, device=dev, dtype=dtype).transpose(1, 2)
+        self.v = torch.randn(B, T, K, D, generator=g, device=dev, dtype=dtype).transpose(1, 2)
+        self.wq = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(dtype).float()
+        self.wk = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(dtype).float()
+        import oracle
+
+        cos, sin = oracle.rope_tables(D, T, theta)
+        self.cos, self.sin = cos.to(dev), sin.to(dev)
+        self.kc = torch.zeros(B, K, T, D, device=dev, dtype=dtype)
+        self.vc = torch.zeros_like(self.kc)
+        self.out = torch.empty(B, T, H, D, device=dev, dtype=dtype)
+        self.scale = 1.0 / math.sqrt(D)
+
+    def append(self):
+        from sleuth_amd import ops
+
+        ops.kv_append(self.k, self.v, self.kc, self.vc, pos=0, k_weight=self.wk, eps=1e-6, norm_k=True,
+                      cos=self.cos, sin=self.sin)
+
+    def attend(self):
+        from sleuth_amd import ops
+
+        return ops.attn_prefill(self.q, self.kc, self.vc, scale=self.scale, offset=0, q_weight=self.wq,
+                                eps=1e-6, norm_q=True, cos=self.cos, sin=self.sin, out=self.out)
+
+    def step(self):
+        self.append()
+        self.attend()
+
+    def flops(self) -> float:
+        """4 * hd * sum over (b, h, query) of the keys it sees (causal: T(T+1)/2)."""
+        return 4.0 * self.D * self.B * self.H * self.T * (self.T + 1) / 2
+
+
+# ----------------------------------------------------------------------------- timing
+def time_loop(fn, steps: int, warmup: int) -> float:
+    """Seconds per call of fn, with HIP events on torch's current stream (the stream
+    every kernel of this package is launched on)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / 1e3 / steps
+
+
+def read_traffic(name: str):
+    """HBM traffic per launch measured with rocprofv3 --pmc (profiles/<name>.json), or None."""
+    p = ROOT / "profiles" / f"{name}.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+def cpu_info() -> dict:
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": model, "logical": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+
+
+def cpu_baseline_decode(wl: DecodeWorkload, budget_s: float = 15.0) -> dict:
+    """The oracle's eager CPU path (torch SDPA on the host, bf16, one SDPA per row over
+    its prefix, attention.py:171-193) on the first rows of the same batch: add rows
+    until about budget_s of CPU work, then report GB/s of algorithmic bytes."""
+    import oracle
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    B, H, K, D = wl.B, wl.H, wl.K, wl.D
+    q = oracle.head_norm_rope(wl.q.cpu(), wl.wq.cpu(), 1e-6, wl.cos.cpu(), wl.sin.cpu())
+    layer = wl.k_caches[0], wl.v_caches[0]
+    rows, total_b, total_t = 0, 0, 0.0
+    s = torch.finfo(wl.dtype).bits // 8
+    for b in range(B):
+        L = wl.lens[b]
+        kc = layer[0][b:b + 1, :, :L].cpu()
+        vc = layer[1][b:b + 1, :, :L].cpu()
+        oracle.ragged_decode(q[b:b + 1], kc, vc, [L], wl.window, wl.scale)  # warm
+        t0 = time.perf_counter()
+        reps = 3
+        for _ in range(reps):
+            oracle.ragged_decode(q[b:b + 1], kc, vc, [L], wl.window, wl.scale)
+        dt = (time.perf_counter() - t0) / reps
+        rows += 1
+        total_t += dt
+        total_b += 2 * K * wl.visible(L) * D * s + 2 * H * wl.T * D * s
+        if total_t * (reps + 1) > budget_s:
+            break
+    return {"value": round(total_b / total_t / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"rows 0..{rows - 1} of the C4 batch ({sum(wl.lens[:rows])} cached tokens), one layer, "
+                      f"bf16 torch SDPA on the host CPU, median-free mean of 3 runs per row",
+            "cpu": cpu_info()}
+
+
+def cpu_baseline_prefill(B, T, H, K, D, budget_s: float = 10.0) -> dict:
+    """torch SDPA (is_causal, enable_gqa) on the host in bf16 at the C3 shape, one
+    batch row (the sample), TFLOP/s."""
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(1, H, T, D, generator=g).bfloat16()
+    k = torch.randn(1, K, T, D, generator=g).bfloat16()
+    v = torch.randn(1, K, T, D, generator=g).bfloat16()
+    f = lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,  # noqa: E731
+                                                                  enable_gqa=True, scale=D ** -0.5)
+    f()
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < budget_s / 2 or n < 2:
+        f()
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    fl = 4.0 * D * H * T * (T + 1) / 2
+    return {"value": round(fl / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"1 of the {B} batch rows ({T} tokens causal), bf16 torch SDPA, mean of {n} runs"}
+
+
+# ----------------------------------------------------------------------------- main
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--extra", action="store_true", help="also print lines for configs C2, C3-decode, C5")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--only", choices=["decode", "prefill"], help="time one workload (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the attention hot path runs on a single MI355X here "
+              "(multi-GPU sharding is design-only). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    dt = torch.bfloat16
+
+    if args.only:
+        return run_only(args, dev)
+
+    # ---- C4 ragged decode (headline)
+    lens = c4_lengths(args.seed)
+    wl = DecodeWorkload(lens, 16, 8, 128, 1e6, dt, dev, seed=args.seed)
+    wl.append()  # write the new tokens once so the rows are complete before timing
+    torch.cuda.synchronize()
+    print(f"[bench] C4 decode: B=64, sum L = {sum(lens)}, chunk {wl.chunk}", file=sys.stderr, flush=True)
+    t_step = time_loop(wl.step, args.steps, args.warmup)
+    t_attn = time_loop(wl.attend, args.steps, args.warmup)
+    step_gbs = wl.step_bytes() / t_step / 1e9
+    attn_gbs = wl.attend_bytes() / t_attn / 1e9
+    tok_s = wl.B / (N_LAYERS * t_step)
+    print(f"[bench] C4 step {t_step * 1e6:.1f} us ({step_gbs:.0f} GB/s), attention call "
+          f"{t_attn * 1e6:.1f} us ({attn_gbs:.0f} GB/s)", file=sys.stderr, flush=True)
+
+    # ---- C3 prefill
+    pf = PrefillWorkload(4, 4096, 16, 8, 128, 1e6, dt, dev)
+    pf.append()
+    t_pstep = time_loop(pf.step, max(3, args.steps // 2), max(1, args.warmup // 2))
+    t_pattn = time_loop(pf.attend, max(3, args.steps // 2), max(1, args.warmup // 2))
+    p_tflops = pf.flops() / t_pattn / 1e12
+    print(f"[bench] C3 prefill step {t_pstep * 1e6:.1f} us, attention kernel {t_pattn * 1e6:.1f} us "
+          f"({p_tflops:.0f} TFLOP/s)", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": METRIC,
+        "value": round(step_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "C4 ragged decode, one layer per step: batch 64, 16 q / 8 kv heads, head dim 128, "
+                               "bf16, KV lengths U[1024, 32768] (seed 0), 1 new token per row, QK-norm, "
+                               "RoPE theta 1e6",
+                   "global_batch": wl.B, "kv_tokens": sum(lens), "chunk": wl.chunk,
+                   "parallelism": "single GPU"},
+        "decode_tokens_per_s": round(tok_s, 1),
+        "decode_attention_call_us": round(t_attn * 1e6, 2),
+        "prefill_tflops": round(p_tflops, 1),
+        "prefill_step_ms": round(t_pstep * 1e3, 4),
+        "prefill_config": "C3: 4 x 4096 causal, 16 q / 8 kv heads, head dim 128, bf16, QK-norm, RoPE theta 1e6",
+        "roofline": {"bound": "hbm", "kernel": "forge::splitk_kernel + combine_kernel (one forge_attn_decode call)",
+                     "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic("decode_c4_traffic"),
+                     "algorithmic_bytes": wl.attend_bytes()},
+        "roofline_prefill": {"bound": "mfma", "kernel": "forge::prefill_kernel<bf16,128>",
+                             "achieved": round(p_tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(p_tflops / BF16_PEAK_TFLOPS, 4),
+                             "traffic": read_traffic("prefill_c3_traffic"), "flops": pf.flops()},
+    }
+    if not args.no_cpu:
+        print("[bench] CPU baseline (decode sample) ...", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline_decode(wl)
+        print("[bench] CPU baseline (prefill sample) ...", file=sys.stderr, flush=True)
+        line["cpu_baseline_prefill"] = cpu_baseline_prefill(4, 4096, 16, 8, 128)
+    else:
+        line["cpu_baseline"] = None
+    if args.extra:
+        line["extra"] = extra_configs(dev, args)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def run_only(args, dev) -> int:
+    """One workload's step loop and nothing else, for rocprofv3 runs."""
+    if args.only == "decode":
+        wl = DecodeWorkload(c4_lengths(args.seed), 16, 8, 128, 1e6, torch.bfloat16, dev, seed=args.seed)
+        wl.append()
+        t = time_loop(wl.step, args.steps, args.warmup)
+        print(json.dumps({"workload": "C4 decode step", "us": round(t * 1e6, 2),
+                          "GBs": round(wl.step_bytes() / t / 1e9, 1)}), flush=True)
+    else:
+        pf = PrefillWorkload(4, 4096, 16, 8, 128, 1e6, torch.bfloat16, dev)
+        t = time_loop(pf.step, args.steps, args.warmup)
+        print(json.dumps({"workload": "C3 prefill step", "us": round(t * 1e6, 2)}), flush=True)
+    return 0
+
+
+def extra_configs(dev, args) -> dict:
+    """Configs C2, C3-decode and C5 (reported, no targets). Small working sets rotate
+    through several layer caches so the ~256 MB MALL does not serve them."""
+    out = {}
+    dt = torch.bfloat16
+    for name, kw in {
+        "C2_decode_b16_12q4kv_hd64_S2048": dict(lens=[2049] * 16, H=12, K=4, D=64, theta=1e4, n_layers=12),
+        "C3_decode_b32_16q8kv_hd128_S8192": dict(lens=[8192] * 32, H=16, K=8, D=128, theta=1e6, n_layers=1),
+        "C5_verify_b8_T4_8q1kv_hd256_global": dict(lens=[8196] * 8, H=8, K=1, D=256, theta=1e6, T=4, n_layers=12),
+        "C5_verify_b8_T4_8q1kv_hd256_window1024": dict(lens=[8196] * 8, H=8, K=1, D=256, theta=1e6, T=4,
+                                                       window=1024, n_layers=12),
+    }.items():
+        lens = kw.pop("lens")
+        wl = DecodeWorkload(lens, dtype=dt, dev=dev, **kw)
+        for i in range(len(wl.k_caches)):
+            wl.append(i)
+        torch.cuda.synchronize()
+        t = time_loop(wl.step, args.steps * 4, args.warmup)
+        ta = time_loop(lambda: (wl.attend(), setattr(wl, "layer", (wl.layer + 1) % len(wl.k_caches))),
+                       args.steps * 4, args.warmup)
+        out[name] = {"step_us": round(t * 1e6, 2), "step_GBs": round(wl.step_bytes() / t / 1e9, 1),
+                     "attention_call_us": round(ta * 1e6, 2),
+                     "attention_GBs": round(wl.attend_bytes() / ta / 1e9, 1), "chunk": wl.chunk}
+        print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
+        del wl
+        torch.cuda.empty_cache()
+    return out
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -9,18 +9,21 @@
 //
 // Inside a block, LPR = D / VEC lanes share one key row: each lane loads 16 bytes
 // (VEC elements) of K and of V with one 128-bit load, so a group of LPR lanes reads a
-// whole row and a wave reads 64 / LPR consecutive rows - fully coalesced. Each group
-// takes NK consecutive keys per iteration (all loads issued before any math), scores
-// them with a DPP butterfly sum over its LPR lanes, and keeps an online-softmax state
-// (m, l, o) per row. The groups are then merged (xor-shuffles inside a wave, LDS across
-// the 4 waves, in a fixed order), and the block writes either the final output (the
-// row sees only this chunk) or an fp32 partial (m, l, o) for the combine kernel.
+// whole row. Per iteration, group g takes the NK keys kb0 + u*NG + g (u < NK), so each
+// load instruction of a wave reads 64 / LPR consecutive rows (1 KB for D = 128). The
+// next iteration's K/V loads are issued before the current one is scored (two register
+// buffers), and the first ones before the q prologue, so HBM latency overlaps the math.
+// Scores use v_dot2_f32_{bf16,f16} on packed q/k pairs and a DPP butterfly over the LPR
+// lanes; the online softmax keeps a reference max that only moves when a score exceeds
+// it by 2^8 (kRescaleLog2), so the rescale of (l, o) is rare. Groups are then merged
+// (xor-shuffles in a wave, LDS across the 4 waves, fixed order) and the block writes the
+// final output (the row sees only this chunk) or an fp32 partial (m, l, o).
 //
 // Determinism: the key -> (group, slot) assignment depends only on the key's absolute
 // position, a key outside a row's visible range is an exact no-op on that row's state
-// (score -inf -> weight 0, max unchanged -> rescale 2^0 = 1), and merges run in a fixed
-// order. So a row's output does not depend on T or on the other rows in the call: a
-// verify row equals the decode of that token alone, bit for bit (same chunk).
+// (score -inf -> weight 0, reference max unchanged), and merges run in a fixed order. So
+// a row's output does not depend on T or on the other rows in the call: a verify row
+// equals the decode of that token alone, bit for bit (same chunk).
 #include <limits.h>
 
 #include "common.h"
@@ -31,6 +34,7 @@ namespace forge {
 constexpr int kSplitThreads = 256;
 constexpr int kSplitNK = 4;  // keys per group per iteration
 constexpr int kMaxChunk = 512;
+constexpr float kRescaleLog2 = 8.0f;  // lazy rescale: weights stay <= 2^8
 
 struct SplitParams {
   const void* q;
@@ -60,6 +64,9 @@ struct SplitParams {
   float* ws_o;    // [B*H*T][max_chunks][D]
 };
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
 // Visible key range [kmin, kmax] of the query at absolute position qpos.
 __device__ __forceinline__ void visible_range(int64_t qpos, int window, int64_t max_len,
                                               int64_t& kmin, int64_t& kmax) {
@@ -68,13 +75,68 @@ __device__ __forceinline__ void visible_range(int64_t qpos, int window, int64_t 
   if (kmin < 0) kmin = 0;
 }
 
+__device__ __forceinline__ void visible_range32(int qpos, int window, int max_len, int& kmin,
+                                                int& kmax) {
+  kmax = qpos < max_len - 1 ? qpos : max_len - 1;
+  kmin = window > 0 ? qpos - window + 1 : 0;
+  if (kmin < 0) kmin = 0;
+}
+
+// q . k over one lane's 16 bytes. bf16/fp16: packed dot2 on the raw pairs (products
+// exact in fp32); fp32: four FMAs.
+template <typename T>
+__device__ __forceinline__ float dot16(const uint4& qraw, const uint4& kraw, float acc) {
+  const unsigned qa[4] = {qraw.x, qraw.y, qraw.z, qraw.w};
+  const unsigned ka[4] = {kraw.x, kraw.y, kraw.z, kraw.w};
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = fmaf(__uint_as_float(qa[j]), __uint_as_float(ka[j]), acc);
+  } else if constexpr (__is_same(T, bf16)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qa[j]),
+                                            __builtin_bit_cast(bf16x2_t, ka[j]), acc, false);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qa[j]),
+                                   __builtin_bit_cast(f16x2_t, ka[j]), acc, false);
+  }
+  return acc;
+}
+
+// 16 bytes of V as VEC floats (bf16 -> fp32 is a shift / mask of the raw bits).
+template <typename T>
+__device__ __forceinline__ void unpack_v(const uint4& raw, float* out) {
+  if constexpr (__is_same(T, bf16)) {
+    const unsigned w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      out[2 * j] = __uint_as_float(w[j] << 16);
+      out[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+    }
+  } else {
+    unpack16<T>(raw, out);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ uint4 load_nt(const T* p) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Loads one q row slice (VEC values at li*VEC), with the optional fused RMSNorm + RoPE,
-// rounded once to T (the dtype the reference's q has when SDPA reads it).
+// rounded once to T (the dtype the reference's q has when SDPA reads it); returned as
+// the raw 16 bytes (packed pairs for dot2).
 template <typename T, int D, int VEC, int LPR>
-__device__ __forceinline__ void load_q_row(const SplitParams& p, int b, int h, int t, int li,
-                                           float* q) {
+__device__ __forceinline__ uint4 load_q_row(const SplitParams& p, int b, int h, int t, int li) {
   const T* src = static_cast<const T*>(p.q) + b * p.sqb + h * p.sqh + t * p.sqt + li * VEC;
-  unpack16<T>(load16(src), q);
+  const uint4 raw = load16(src);
+  if (!(p.flags & (FORGE_NORM_QK | FORGE_ROPE))) return raw;
+  float q[VEC];
+  unpack16<T>(raw, q);
   if (p.flags & FORGE_NORM_QK) {
     float ss = 0.0f;
 #pragma unroll
@@ -102,8 +164,7 @@ __device__ __forceinline__ void load_q_row(const SplitParams& p, int b, int h, i
 #pragma unroll
     for (int e = 0; e < VEC; ++e) q[e] = y[e];
   }
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) q[e] = to_f32<T>(from_f32<T>(q[e]));
+  return pack16<T>(q);
 }
 
 template <typename T, int D, int ROWS>
@@ -112,7 +173,6 @@ __global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
   constexpr int LPR = D / VEC;  // lanes per key row
   static_assert(LPR >= 2 && LPR <= kWave && (LPR & (LPR - 1)) == 0, "bad head dim");
   constexpr int NG = kSplitThreads / LPR;  // key groups per block
-  constexpr int GPW = kWave / LPR;         // key groups per wave
   constexpr int NK = kSplitNK;
   constexpr int KPI = NG * NK;  // keys per block iteration
   constexpr int NWAVES = kSplitThreads / kWave;
@@ -130,38 +190,67 @@ __global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
   const int rb = blockIdx.y / p.K;
   const int b = blockIdx.z;
 
-  const int64_t base = row_base(p.row_pos, p.pos_dev, p.pos0, b);
+  // Positions fit in 32 bits (host check: max_len < 2^31).
+  const int base = (int)row_base(p.row_pos, p.pos_dev, p.pos0, b);
 
-  // Rows of this block and their visible key ranges.
-  int64_t kmin[ROWS], kmax[ROWS];
-  int hrow[ROWS], trow[ROWS];
-  bool valid[ROWS];
-  int64_t kmin_rb = LLONG_MAX, kmax_rb = -1;
+  // Rows of this block and their visible key ranges; the union [kmin_rb, kmax_rb] and
+  // the intersection [lo_all, hi_all] over the valid rows.
+  int kmin[ROWS], kmax[ROWS];
+  int kmin_rb = INT_MAX, kmax_rb = -1, lo_all = -1, hi_all = INT_MAX;
 #pragma unroll
   for (int r = 0; r < ROWS; ++r) {
     const int flat = rb * ROWS + r;
-    valid[r] = flat < p.rows_total;
-    trow[r] = valid[r] ? flat / p.G : 0;
-    hrow[r] = kvh * p.G + (valid[r] ? flat % p.G : 0);
-    visible_range(base + trow[r], p.window, p.max_len, kmin[r], kmax[r]);
-    if (!valid[r]) {
-      kmin[r] = LLONG_MAX;
+    if (flat < p.rows_total) {
+      visible_range32(base + flat / p.G, p.window, (int)p.max_len, kmin[r], kmax[r]);
+      kmin_rb = kmin[r] < kmin_rb ? kmin[r] : kmin_rb;
+      kmax_rb = kmax[r] > kmax_rb ? kmax[r] : kmax_rb;
+      lo_all = kmin[r] > lo_all ? kmin[r] : lo_all;
+      hi_all = kmax[r] < hi_all ? kmax[r] : hi_all;
+    } else {
+      kmin[r] = INT_MAX;
       kmax[r] = -1;
     }
-    kmin_rb = kmin[r] < kmin_rb ? kmin[r] : kmin_rb;
-    kmax_rb = kmax[r] > kmax_rb ? kmax[r] : kmax_rb;
   }
-  const int64_t c0 = (int64_t)c * p.chunk;
+  const int c0 = c * p.chunk;
   if (c0 > kmax_rb || c0 + p.chunk - 1 < kmin_rb) return;  // block-uniform
+  const int iters = p.chunk / KPI;
+  int it_first = kmin_rb > c0 ? (kmin_rb - c0) / KPI : 0;
+  int it_last = (kmax_rb - c0) / KPI;
+  if (it_last > iters - 1) it_last = iters - 1;
 
-  float q[ROWS][VEC];
+  // One (b, kv head) slab of the cache; offsets inside it fit in 32 bits (host check).
+  const T* kbase = static_cast<const T*>(p.kc) + b * p.skb + kvh * p.skh + li * VEC;
+  const T* vbase = static_cast<const T*>(p.vc) + b * p.skb + kvh * p.skh + li * VEC;
+  const int sks = (int)p.sks;
+
+  // Loads of iteration `it`; keys outside [kmin_rb, kmax_rb] are not read.
+  auto load_iter = [&](int it, uint4* kr, uint4* vr) {
+    const int kb0 = c0 + it * KPI;
+    const bool inside = kb0 >= kmin_rb && kb0 + KPI - 1 <= kmax_rb;
+#pragma unroll
+    for (int u = 0; u < NK; ++u) {
+      const int kp = kb0 + u * NG + g;
+      if (inside || (kp >= kmin_rb && kp <= kmax_rb)) {
+        kr[u] = load_nt(kbase + kp * sks);
+        vr[u] = load_nt(vbase + kp * sks);
+      } else {
+        kr[u] = make_uint4(0, 0, 0, 0);
+        vr[u] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+
+  uint4 ka[NK], va[NK], kb[NK], vb[NK];
+  load_iter(it_first, ka, va);
+
+  uint4 q[ROWS];
 #pragma unroll
   for (int r = 0; r < ROWS; ++r) {
-    if (valid[r]) {
-      load_q_row<T, D, VEC, LPR>(p, b, hrow[r], trow[r], li, q[r]);
+    const int flat = rb * ROWS + r;
+    if (flat < p.rows_total) {
+      q[r] = load_q_row<T, D, VEC, LPR>(p, b, kvh * p.G + flat % p.G, flat / p.G, li);
     } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) q[r][e] = 0.0f;
+      q[r] = make_uint4(0, 0, 0, 0);
     }
   }
 
@@ -174,73 +263,66 @@ __global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
     for (int e = 0; e < VEC; ++e) o[r][e] = 0.0f;
   }
 
-  const T* kbase = static_cast<const T*>(p.kc) + b * p.skb + kvh * p.skh + li * VEC;
-  const T* vbase = static_cast<const T*>(p.vc) + b * p.skb + kvh * p.skh + li * VEC;
-  const int iters = p.chunk / KPI;
-  for (int it = 0; it < iters; ++it) {
-    const int64_t kb0 = c0 + (int64_t)it * KPI;
-    if (kb0 > kmax_rb || kb0 + KPI - 1 < kmin_rb) continue;  // block-uniform
-    const int64_t kg0 = kb0 + g * NK;
-    uint4 kraw[NK], vraw[NK];
-#pragma unroll
-    for (int u = 0; u < NK; ++u) {
-      const int64_t kp = kg0 + u;
-      if (kp >= kmin_rb && kp <= kmax_rb) {
-        kraw[u] = load16(kbase + kp * p.sks);
-        vraw[u] = load16(vbase + kp * p.sks);
-      } else {
-        kraw[u] = make_uint4(0, 0, 0, 0);
-        vraw[u] = make_uint4(0, 0, 0, 0);
-      }
-    }
-    float kf[NK][VEC];
-#pragma unroll
-    for (int u = 0; u < NK; ++u) unpack16<T>(kraw[u], kf[u]);
-
+  auto compute_iter = [&](int it, const uint4* kr, const uint4* vr) {
+    const int kb0 = c0 + it * KPI;
+    const bool full = kb0 >= lo_all && kb0 + KPI - 1 <= hi_all;  // every row sees every key
     float s[ROWS][NK];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
 #pragma unroll
-      for (int u = 0; u < NK; ++u) {
-        float d = 0.0f;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) d += q[r][e] * kf[u][e];
-        s[r][u] = group_sum<LPR>(d) * p.scale_log2;
-        const int64_t kp = kg0 + u;
-        if (kp < kmin[r] || kp > kmax[r]) s[r][u] = kNegInf;
-      }
+      for (int u = 0; u < NK; ++u) s[r][u] = group_sum<LPR>(dot16<T>(q[r], kr[u], 0.0f)) * p.scale_log2;
     }
-
+    if (!full) {
+#pragma unroll
+      for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int u = 0; u < NK; ++u) {
+          const int kp = kb0 + u * NG + g;
+          if (kp < kmin[r] || kp > kmax[r]) s[r][u] = kNegInf;
+        }
+    }
     float vf[NK][VEC];
 #pragma unroll
-    for (int u = 0; u < NK; ++u) unpack16<T>(vraw[u], vf[u]);
+    for (int u = 0; u < NK; ++u) unpack_v<T>(vr[u], vf[u]);
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
       float mx = s[r][0];
 #pragma unroll
       for (int u = 1; u < NK; ++u) mx = fmaxf(mx, s[r][u]);
-      const float m_new = fmaxf(m[r], mx);
-      const float alpha = rescale(m[r], m_new);
-      float pu[NK];
+      if (mx > m[r] + kRescaleLog2) {  // (m = -inf: first visible key)
+        const float alpha = m[r] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(m[r] - mx);
+        l[r] *= alpha;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[r][e] *= alpha;
+        m[r] = mx;
+      }
       float psum = 0.0f;
+      float pu[NK];
 #pragma unroll
       for (int u = 0; u < NK; ++u) {
-        pu[u] = exp2_masked(s[r][u], m_new);
+        pu[u] = s[r][u] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(s[r][u] - m[r]);
         psum += pu[u];
       }
-      l[r] = l[r] * alpha + psum;
+      l[r] += psum;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        float acc = o[r][e] * alpha;
+        float acc = o[r][e];
 #pragma unroll
-        for (int u = 0; u < NK; ++u) acc += pu[u] * vf[u][e];
+        for (int u = 0; u < NK; ++u) acc = fmaf(pu[u], vf[u][e], acc);
         o[r][e] = acc;
       }
-      m[r] = m_new;
     }
+  };
+
+  for (int it = it_first; it <= it_last; it += 2) {
+    if (it + 1 <= it_last) load_iter(it + 1, kb, vb);
+    compute_iter(it, ka, va);
+    if (it + 1 > it_last) break;
+    if (it + 2 <= it_last) load_iter(it + 2, ka, va);
+    compute_iter(it + 1, kb, vb);
   }
 
-  // Merge the GPW groups of this wave: butterfly over lane distances LPR .. 32.
+  // Merge the groups of this wave: butterfly over lane distances LPR .. 32.
 #pragma unroll
   for (int dist = LPR; dist < kWave; dist <<= 1) {
 #pragma unroll
@@ -259,7 +341,6 @@ __global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
       m[r] = m_n;
     }
   }
-  (void)GPW;
   if (tid % kWave < LPR) {
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
@@ -277,13 +358,12 @@ __global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
   for (int idx = tid; idx < ROWS * D; idx += kSplitThreads) {
     const int r = idx / D;
     const int e = idx % D;
-    if (r >= ROWS) break;
     const int flat = rb * ROWS + r;
     if (flat >= p.rows_total) continue;
     const int t = flat / p.G;
     const int h = kvh * p.G + flat % p.G;
-    int64_t rkmin, rkmax;
-    visible_range(base + t, p.window, p.max_len, rkmin, rkmax);
+    int rkmin, rkmax;
+    visible_range32(base + t, p.window, (int)p.max_len, rkmin, rkmax);
     if (c0 > rkmax || c0 + p.chunk - 1 < rkmin) continue;  // this chunk is outside the row
     float M = sh_m[0][r];
 #pragma unroll
@@ -295,8 +375,8 @@ __global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
       L = L + a * sh_l[w][r];
       O = O + a * sh_o[w][r][e];
     }
-    const int64_t cmin = rkmin / p.chunk;
-    const int64_t cmax = rkmax / p.chunk;
+    const int cmin = rkmin / p.chunk;
+    const int cmax = rkmax / p.chunk;
     if (cmin == cmax) {
       T* dst = static_cast<T*>(p.out) + b * p.sob + t * p.sot + h * p.soh;
       dst[e] = from_f32<T>(O / L);
@@ -309,15 +389,19 @@ __global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
   }
 }
 
-// One wave per (b, h, t) row: merges the row's chunk partials in chunk order.
+// One block (4 waves) per (b, h, t) row: wave w merges chunks w, w+4, ... of the row
+// (8 at a time, loads issued together), then the 4 wave results are merged in order.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void combine_kernel(SplitParams p) {
   constexpr int EPL = D >= kWave ? D / kWave : 1;  // elements per lane
+  constexpr int NWAVES = 4;
+  constexpr int UNROLL = 8;
+  __shared__ float sh_o[NWAVES][D];
+  __shared__ float sh_m[NWAVES], sh_l[NWAVES];
   const int lane = threadIdx.x % kWave;
-  const int64_t row = (int64_t)blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
-  if (row >= (int64_t)p.B * p.H * p.T) return;
+  const int wave = threadIdx.x / kWave;
+  const int64_t row = blockIdx.x;  // == (b*H + h)*T + t
   const int t = (int)(row % p.T);
-  const int h = (int)((row / p.T) % p.H);
   const int b = (int)(row / ((int64_t)p.T * p.H));
   const int64_t base = row_base(p.row_pos, p.pos_dev, p.pos0, b);
   int64_t kmin, kmax;
@@ -327,30 +411,61 @@ __global__ __launch_bounds__(256) void combine_kernel(SplitParams p) {
   int64_t cmax = kmax / p.chunk;
   if (cmax > p.max_chunks - 1) cmax = p.max_chunks - 1;
   if (cmin >= cmax) return;  // single chunk: the split kernel wrote the output
-  const int64_t slot0 = row * p.max_chunks;  // row == (b*H + h)*T + t
+  const int64_t slot0 = row * p.max_chunks;
 
   float M = kNegInf;
-  for (int64_t c = cmin + lane; c <= cmax; c += kWave) M = fmaxf(M, p.ws_ml[slot0 + c].x);
+  for (int64_t c = cmin + threadIdx.x; c <= cmax; c += 256) M = fmaxf(M, p.ws_ml[slot0 + c].x);
   M = group_max<kWave>(M);
+  if (lane == 0) sh_m[wave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(sh_m[0], sh_m[1]), fmaxf(sh_m[2], sh_m[3]));
+  __syncthreads();
 
+  const bool active = lane * EPL < D;
   float L = 0.0f, O[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) O[i] = 0.0f;
-  const bool active = lane * EPL < D;
-  for (int64_t c = cmin; c <= cmax; ++c) {
-    const float2 ml = p.ws_ml[slot0 + c];
-    const float a = rescale(ml.x, M);
-    L = L + a * ml.y;
-    if (active) {
-      const float* src = p.ws_o + (slot0 + c) * D + lane * EPL;
+  for (int64_t c = cmin + wave; c <= cmax; c += NWAVES * UNROLL) {
+    float2 ml[UNROLL];
+    float ov[UNROLL][EPL];
 #pragma unroll
-      for (int i = 0; i < EPL; ++i) O[i] = O[i] + a * src[i];
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t cc = c + (int64_t)u * NWAVES;
+      if (cc <= cmax) {
+        ml[u] = p.ws_ml[slot0 + cc];
+        const float* src = p.ws_o + (slot0 + cc) * D + lane * EPL;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) ov[u][i] = active ? src[i] : 0.0f;
+      } else {
+        ml[u] = make_float2(kNegInf, 0.0f);
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) ov[u][i] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const float a = rescale(ml[u].x, M);
+      L = L + a * ml[u].y;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) O[i] = O[i] + a * ov[u][i];
     }
   }
-  if (!active) return;
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) sh_o[wave][lane * EPL + i] = O[i];
+  }
+  if (lane == 0) sh_l[wave] = L;
+  __syncthreads();
+  if (wave != 0 || !active) return;
+  const float Lt = ((sh_l[0] + sh_l[1]) + sh_l[2]) + sh_l[3];
+  const int h = (int)((row / p.T) % p.H);
   T* dst = static_cast<T*>(p.out) + b * p.sob + t * p.sot + h * p.soh + lane * EPL;
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) dst[i] = from_f32<T>(O[i] / L);
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane * EPL + i;
+    const float Ot = ((sh_o[0][e] + sh_o[1][e]) + sh_o[2][e]) + sh_o[3][e];
+    dst[i] = from_f32<T>(Ot / Lt);
+  }
 }
 
 // ---------------------------------------------------------------- host side
@@ -390,8 +505,8 @@ static int launch_split_d(const SplitParams& p, int rows, dim3 grid, hipStream_t
   int st = check_launch();
   if (st || p.max_chunks < 2) return st;
   const int64_t nrows = (int64_t)p.B * p.H * p.T;
-  const dim3 cgrid((unsigned)((nrows + 3) / 4));
-  hipLaunchKernelGGL((combine_kernel<T, D>), cgrid, dim3(256), 0, s, p);
+  if (nrows > 0x7fffffff) return set_error("too many rows");
+  hipLaunchKernelGGL((combine_kernel<T, D>), dim3((unsigned)nrows), dim3(256), 0, s, p);
   return check_launch();
 }
 
@@ -418,7 +533,6 @@ extern "C" int forge_attn_decode_chunk(int dtype, int B, int T, int H, int K, in
 
 extern "C" size_t forge_attn_decode_workspace_bytes(int dtype, int B, int T, int H, int K,
                                                     int D, int64_t max_kv_len, int chunk) {
-  (void)K;
   if (chunk <= 0) chunk = (K > 0 && H % K == 0) ? auto_chunk(dtype, B, T, H, K, D, max_kv_len) : 64;
   const int64_t max_chunks = (max_kv_len + chunk - 1) / chunk;
   if (max_chunks < 2) return 0;
@@ -444,7 +558,14 @@ extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, c
   if (!head_dim_ok(D)) return set_error("forge_attn_decode: head dim must be 32, 64, 128 or 256");
   if (!q || !k_cache || !v_cache || !out) return set_error("null tensor pointer");
   if ((flags & FORGE_ROPE) && (!cos || !sin)) return set_error("FORGE_ROPE needs cos and sin");
-  if (max_len <= 0) return set_error("cache length must be positive");
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16)
+    return set_error("forge_attn_decode: q and the caches must be 16-byte aligned");
+  const int vec = vec_of(dtype);
+  if ((sqb | sqh | sqt | skb | skh | sks) % vec)
+    return set_error("forge_attn_decode: q/cache strides must be multiples of 16 bytes");
+  if (max_len <= 0 || max_len >= (1LL << 30)) return set_error("cache length must be in [1, 2^30)");
+  if (sks * (max_len + 1) >= (1LL << 31))
+    return set_error("forge_attn_decode: one (batch, kv head) slab of the cache must hold < 2^31 elements");
   if (max_kv_len <= 0 || max_kv_len > max_len) max_kv_len = max_len;
   if (!row_pos && !pos_dev && (pos0 < 0 || pos0 + T > max_len))
     return set_error("KV cache full: pos + T exceeds the cache length");

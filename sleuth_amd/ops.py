@@ -59,7 +59,10 @@ def _weight(w: torch.Tensor | None, D: int) -> torch.Tensor | None:
         return None
     if w.numel() != D:
         raise ValueError(f"norm gain has {w.numel()} values for head dim {D}")
-    return w.detach().to(torch.float32).contiguous()
+    w = w.detach()
+    if w.dtype == torch.float32 and w.is_contiguous():
+        return w
+    return w.to(torch.float32).contiguous()
 
 
 def _rope_tables(cos, sin, B: int, T: int, D: int):
