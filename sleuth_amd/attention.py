@@ -1,0 +1,245 @@
+"""Grouped-query attention with QK-norm, RoPE and a KV cache: the drop-in for
+sleuth/forge/model/attention.py:76-206.
+
+Same constructor (cfg, layer_idx), submodule names (q_proj/k_proj/v_proj/o_proj/q_norm/
+k_norm, the loaders' contract), taps (tap_q, tap_k, tap_pattern, tap_z) and forward
+signature forward(x, cos, sin, cache=None, same_doc=None) -> [B, T, d].
+
+Paths (the reference's own dispatch, attention.py:109-153, with the HIP kernels in place
+of head_norm_rope + cache.update + SDPA):
+  * HIP (GPU inference: no grad, dtype fp32/bf16/fp16, head dim 32/64/128/256, no
+    partial RoPE, no document mask, nobody listening on attn.pattern):
+      forge_kv_append   k norm + RoPE (+ v norm), written into the cache at pos /
+                        pos_t / per-row lengths;
+      T <= 16           forge_attn_decode (split-K; decode, verify, static steps), q norm
+                        + RoPE fused into its q load;
+      T > 16            forge_attn_prefill (bf16/fp16 MFMA flash, head dim 64/128/256)
+                        else forge_attn_decode (fp32 and other head sizes).
+    The output comes back as [B, T, H, hd], the layout o_proj reads.
+  * torch (CPU, training, partial RoPE, document masks, the pattern tap, or
+    SLEUTH_AMD_NO_HIP=1): the reference's eager code, unchanged in meaning.
+If a GPU tensor would take the HIP path and the library is missing or fails its
+first-use self-check, forward raises: there is no silent fallback.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .config import ModelConfig
+from .norm import RMSNorm
+from .rope import apply_rope
+from .taps import Tap
+
+DECODE_MAX_T = 16
+_HIP_HEAD_DIMS = (32, 64, 128, 256)
+_HIP_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+_checked: dict[tuple, bool] = {}
+
+
+def hip_disabled() -> bool:
+    return os.environ.get("SLEUTH_AMD_NO_HIP") == "1"
+
+
+def _hip_ready(device: torch.device, dtype: torch.dtype) -> None:
+    """First use per (device, dtype): the library must load and pass its self-check."""
+    key = (device.type, device.index, dtype)
+    if key not in _checked:
+        from .selfcheck import self_check
+
+        self_check(device, dtype)   # raises on failure
+        _checked[key] = True
+
+
+class Attention(nn.Module):
+    def __init__(self, cfg: ModelConfig, layer_idx: int):
+        super().__init__()
+        spec = cfg.attn_spec(layer_idx)
+        self.layer_idx = layer_idx
+        self.kind = spec.kind
+        self.n_heads, self.n_kv, self.hd = cfg.n_heads, spec.kv_heads, spec.head_dim
+        self.window = spec.window
+        self.scale = cfg.attn_scale or 1.0 / math.sqrt(self.hd)
+        self.eps = cfg.norm_eps
+        self.use_rope = cfg.pos_type == "rope"
+        self.partial_rope = bool(cfg.rope_dim) and cfg.rope_dim < self.hd
+        qkv_bias = cfg.bias or cfg.qkv_bias
+        self.q_proj = nn.Linear(cfg.d_model, self.n_heads * self.hd, bias=qkv_bias)
+        self.k_proj = nn.Linear(cfg.d_model, self.n_kv * self.hd, bias=qkv_bias)
+        self.v_proj = None if spec.v_from_k else nn.Linear(cfg.d_model, self.n_kv * self.hd, bias=qkv_bias)
+        self.o_proj = nn.Linear(self.n_heads * self.hd, cfg.d_model, bias=cfg.bias)
+        self.q_norm = RMSNorm(self.hd, cfg.norm_eps) if cfg.qk_norm else None
+        self.k_norm = RMSNorm(self.hd, cfg.norm_eps) if cfg.qk_norm else None
+        self.v_norm = cfg.v_norm
+        self.tap_q = Tap()
+        self.tap_k = Tap()
+        self.tap_pattern = Tap()
+        self.tap_z = Tap()
+        self.last_path = ""   # "hip-decode" | "hip-prefill" | "torch" (for tests and stats)
+
+    # ------------------------------------------------------------------ dispatch
+    def _use_hip(self, q: torch.Tensor, cache, same_doc) -> bool:
+        if not q.is_cuda or hip_disabled():
+            return False
+        if torch.is_grad_enabled() and q.requires_grad:
+            return False
+        if self.partial_rope or same_doc is not None or self.tap_pattern.active:
+            return False
+        if q.dtype not in _HIP_DTYPES or self.hd not in _HIP_HEAD_DIMS:
+            return False
+        if cache is not None and cache.k[self.layer_idx].dtype != q.dtype:
+            return False   # the reference's SDPA needs q and the cache in one dtype too
+        _hip_ready(q.device, q.dtype)
+        return True
+
+    def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, cache=None,
+                same_doc=None) -> torch.Tensor:
+        B, T, _ = x.shape
+        q = self.q_proj(x).view(B, T, self.n_heads, self.hd).transpose(1, 2)  # [B, H, T, hd]
+        k = self.k_proj(x).view(B, T, self.n_kv, self.hd).transpose(1, 2)     # [B, K, T, hd]
+        v = k if self.v_proj is None else self.v_proj(x).view(B, T, self.n_kv, self.hd).transpose(1, 2)
+        if self._use_hip(q, cache, same_doc):
+            y = self._forward_hip(q, k, v, cos, sin, cache)
+        else:
+            y = self._forward_torch(q, k, v, cos, sin, cache, same_doc).transpose(1, 2)
+            self.last_path = "torch"
+        y = self.tap_z(y)                # [B, T, H, hd] per-head outputs
+        return self.o_proj(y.reshape(B, T, self.n_heads * self.hd))
+
+    # ------------------------------------------------------------------ HIP path
+    def _forward_hip(self, q, k, v, cos, sin, cache) -> torch.Tensor:
+        from . import ops
+
+        B, H, T, hd = q.shape
+        qn, kn = self.q_norm is not None, self.k_norm is not None
+        rc, rs = (cos, sin) if self.use_rope else (None, None)
+        if rc is not None and rc.dtype != torch.float32:
+            rc, rs = rc.float(), rs.float()
+        qw = self.q_norm.weight_f32() if qn else None
+        kw = self.k_norm.weight_f32() if kn else None
+        if self.tap_q.active or self.tap_k.active:
+            # Listeners see (and may replace) q and k after RoPE: materialise them.
+            if qn or rc is not None:
+                q = ops.head_norm_rope(q, qw, self.eps if qn else 0.0, rc, rs, qn)
+                k = ops.head_norm_rope(k, kw, self.eps if kn else 0.0, rc, rs, kn)
+            q, k = self.tap_q(q), self.tap_k(k)
+            q_args = dict(norm_q=False, cos=None, sin=None)
+            k_args = dict(norm_k=False, cos=None, sin=None)
+        else:
+            q_args = dict(q_weight=qw, eps=self.eps, norm_q=qn, cos=rc, sin=rs)
+            k_args = dict(k_weight=kw, eps=self.eps, norm_k=kn, cos=rc, sin=rs)
+        norm_v = bool(self.v_norm)
+        if q.stride(-1) != 1:
+            q = q.contiguous()
+
+        if cache is None:
+            kc = torch.empty(B, self.n_kv, T, hd, device=q.device, dtype=q.dtype)
+            vc = torch.empty_like(kc)
+            ops.kv_append(k, v, kc, vc, pos=0, norm_v=norm_v, **k_args)
+            pos_kw, max_kv, offset, chunk = dict(pos=0), T, 0, 0
+        else:
+            kc, vc = cache.k[self.layer_idx], cache.v[self.layer_idx]
+            chunk = ops.decode_chunk(q.dtype, B, 1, H, self.n_kv, hd, cache.max_len)
+            if getattr(cache, "static", False):
+                pos = cache.positions
+                pos_kw, max_kv, offset = dict(pos_dev=pos), min(cache.length, cache.max_len), None
+            elif getattr(cache, "ragged", False):
+                cache.check_room(T)
+                pos_kw = dict(row_pos=cache.seq_lens)
+                max_kv, offset = max(cache.seq_lens_host) + T, None
+            else:
+                cache.check_room(T)
+                pos_kw, max_kv, offset = dict(pos=cache.pos), cache.pos + T, cache.pos
+            ops.kv_append(k, v, kc, vc, norm_v=norm_v, **pos_kw, **k_args)
+
+        if T > DECODE_MAX_T and offset is not None and ops.prefill_supported(q) and \
+                (q_args["cos"] is None or q_args["cos"].dim() == 2):
+            self.last_path = "hip-prefill"
+            return ops.attn_prefill(q, kc, vc, scale=self.scale, offset=offset, window=self.window, **q_args)
+        self.last_path = "hip-decode"
+        return ops.attn_decode(q, kc, vc, scale=self.scale, max_kv_len=max_kv, window=self.window,
+                               chunk=chunk, **pos_kw, **q_args)
+
+    # ------------------------------------------------------------------ torch path
+    def _forward_torch(self, q, k, v, cos, sin, cache, same_doc) -> torch.Tensor:
+        """The reference's eager path (attention.py:120-153), returns [B, H, T, hd]."""
+        if self.q_norm is not None:
+            q, k = self.q_norm(q), self.k_norm(k)
+        if self.v_norm:
+            v = F.rms_norm(v.float(), (self.hd,), None, self.eps).to(v.dtype)
+        if self.use_rope:
+            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+        q, k = self.tap_q(q), self.tap_k(k)
+        if cache is not None and getattr(cache, "ragged", False) and not getattr(cache, "static", False):
+            return self._ragged_torch(q, k, v, cache, same_doc)
+        if cache is not None:
+            k, v = cache.update(self.layer_idx, k, v)
+        S = k.shape[2]
+        offset = S - q.shape[2]
+        if getattr(cache, "static", False) and not self.tap_pattern.active:
+            kwargs = {"enable_gqa": True} if self.n_kv != self.n_heads else {}
+            return F.scaled_dot_product_attention(q, k, v, attn_mask=cache.attn_mask(self.window),
+                                                  scale=self.scale, **kwargs)
+        if self.tap_pattern.active:
+            return self._explicit(q, k, v, offset, same_doc)
+        return self._fused(q, k, v, offset, same_doc)
+
+    def _ragged_torch(self, q, k, v, cache, same_doc):
+        """Per-row torch attention for a cache with per-row lengths."""
+        T = q.shape[2]
+        lens = list(cache.seq_lens_host)
+        cache.update(self.layer_idx, k, v)
+        out = []
+        for b, L in enumerate(lens):
+            kb = cache.k[self.layer_idx][b:b + 1, :, :L + T]
+            vb = cache.v[self.layer_idx][b:b + 1, :, :L + T]
+            fn = self._explicit if self.tap_pattern.active else self._fused
+            out.append(fn(q[b:b + 1], kb, vb, L, same_doc))
+        return torch.cat(out, 0)
+
+    def _mask(self, T: int, S: int, offset: int, device) -> torch.Tensor:
+        """[T, S] bool, True = may attend (attention.py:160-169)."""
+        qpos = torch.arange(T, device=device)[:, None] + offset
+        kpos = torch.arange(S, device=device)[None, :]
+        mask = kpos <= qpos
+        if self.window:
+            mask &= qpos - kpos < self.window
+        return mask
+
+    def _fused(self, q, k, v, offset, same_doc=None):
+        T, S = q.shape[2], k.shape[2]
+        kwargs = {"scale": self.scale}
+        if self.n_kv != self.n_heads:
+            if same_doc is None:
+                kwargs["enable_gqa"] = True
+            else:
+                k = k.repeat_interleave(self.n_heads // self.n_kv, dim=1)
+                v = v.repeat_interleave(self.n_heads // self.n_kv, dim=1)
+        windowed = self.window and S > self.window
+        if same_doc is not None:
+            mask = self._mask(T, S, offset, q.device) & same_doc
+            return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, **kwargs)
+        if offset == 0 and not windowed:
+            return F.scaled_dot_product_attention(q, k, v, is_causal=True, **kwargs)
+        if T == 1 and not windowed:
+            return F.scaled_dot_product_attention(q, k, v, **kwargs)
+        mask = self._mask(T, S, offset, q.device)
+        return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, **kwargs)
+
+    def _explicit(self, q, k, v, offset, same_doc=None):
+        T, S = q.shape[2], k.shape[2]
+        rep = self.n_heads // self.n_kv
+        k = k.repeat_interleave(rep, dim=1)
+        v = v.repeat_interleave(rep, dim=1)
+        scores = (q.float() @ k.float().transpose(-2, -1)) * self.scale
+        mask = self._mask(T, S, offset, q.device)
+        if same_doc is not None:
+            mask = mask & same_doc
+        scores = scores.masked_fill(~mask, float("-inf"))
+        probs = self.tap_pattern(scores.softmax(dim=-1))
+        return (probs @ v.float()).to(q.dtype)

@@ -1,0 +1,282 @@
+"""The drop-in module on the GPU: Attention + KVCache through the HIP kernels against
+the oracle on the same projections, for the BASELINE config shapes; downstream-logit
+argmax; and the callers (chunked prefill, graph decoding, speculative verify, ragged
+batches, taps) behaving as the reference's tests require."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import oracle
+from conftest import gpu_available
+from helpers import max_abs
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
+DEV = "cuda"
+
+
+def _modules():
+    from sleuth_amd.attention import Attention
+    from sleuth_amd.config import ModelConfig
+    from sleuth_amd.kv_cache import KVCache
+
+    return Attention, ModelConfig, KVCache
+
+
+def _run_layer(dtype, d_model, H, K, hd, theta, steps, B=1, window=0, qk_norm=True, v_norm=False,
+               seed=0, lens=None, pos_start=0):
+    """Runs one Attention layer through a cache for the given token counts per call and
+    returns [(got_z [B,T,H,hd], ref [B,T,H,hd], path)] per call. The oracle sees the
+    module's own raw projections (recorded by hooks), normalised with one rounding to
+    the dtype (fused_ops semantics), and attends in fp32 over its own cache."""
+    Attention, ModelConfig, KVCache = _modules()
+    cfg = ModelConfig(vocab_size=10, d_model=d_model, n_heads=H, n_kv_heads=K, head_size=hd,
+                      qk_norm=qk_norm, v_norm=v_norm, rope_theta=theta, n_layers=1,
+                      layer_types=["sliding"] if window else [], sliding_window=window)
+    torch.manual_seed(seed)
+    a = Attention(cfg, 0).eval()
+    if qk_norm:
+        with torch.no_grad():
+            a.q_norm.weight.copy_(1 + 0.1 * torch.randn(hd))
+            a.k_norm.weight.copy_(1 + 0.1 * torch.randn(hd))
+    a = a.to(DEV, dtype)
+    rec = {}
+    a.q_proj.register_forward_hook(lambda m, i, o: rec.__setitem__("q", o))
+    a.k_proj.register_forward_hook(lambda m, i, o: rec.__setitem__("k", o))
+    a.v_proj.register_forward_hook(lambda m, i, o: rec.__setitem__("v", o))
+    seen = {}
+    a.tap_z.listeners.append(lambda n, t: seen.__setitem__("z", t.clone()))
+    max_len = pos_start + sum(steps) + 8 if lens is None else max(lens) + sum(steps) + 8
+    cache = KVCache([(K, hd)], B, max_len, DEV, dtype)
+    ocache = oracle.KVCache([(K, hd)], B, max_len, "cpu", torch.float32)
+    cos_t, sin_t = oracle.rope_tables(hd, max_len, theta)
+    g = torch.Generator().manual_seed(seed + 1)
+    if lens is not None:   # ragged rows, pre-filled with N(0,1) (already normalised K/V)
+        for b, L in enumerate(lens):
+            kv = torch.randn(2, K, L, hd, generator=g).to(dtype)
+            cache.k[0][b, :, :L] = kv[0].to(DEV)
+            cache.v[0][b, :, :L] = kv[1].to(DEV)
+            ocache.k[0][b, :, :L] = kv[0].float()
+            ocache.v[0][b, :, :L] = kv[1].float()
+        cache.set_lengths(lens)
+    elif pos_start:
+        kv = torch.randn(2, B, K, pos_start, hd, generator=g).to(dtype)
+        cache.k[0][:, :, :pos_start] = kv[0].to(DEV)
+        cache.v[0][:, :, :pos_start] = kv[1].to(DEV)
+        ocache.k[0][:, :, :pos_start] = kv[0].float()
+        ocache.v[0][:, :, :pos_start] = kv[1].float()
+        cache.pos = ocache.pos = pos_start
+    qw = a.q_norm.weight.detach().cpu() if qk_norm else None
+    kw = a.k_norm.weight.detach().cpu() if qk_norm else None
+    results = []
+    for T in steps:
+        x = torch.randn(B, T, d_model, generator=g).to(dtype).to(DEV)
+        if lens is None:
+            p0 = [cache.pos] * B
+            cos, sin = cos_t[p0[0]:p0[0] + T], sin_t[p0[0]:p0[0] + T]
+        else:
+            p0 = list(cache.seq_lens_host)
+            cos = torch.stack([cos_t[p:p + T] for p in p0])
+            sin = torch.stack([sin_t[p:p + T] for p in p0])
+        with torch.no_grad():
+            a(x, cos.to(DEV), sin.to(DEV), cache)
+        q = rec["q"].view(B, T, H, hd).transpose(1, 2).cpu()
+        k = rec["k"].view(B, T, K, hd).transpose(1, 2).cpu()
+        v = rec["v"].view(B, T, K, hd).transpose(1, 2).cpu()
+        qn = oracle.head_norm_rope(q, qw, cfg.norm_eps, cos, sin, norm=qk_norm)
+        kn = oracle.head_norm_rope(k, kw, cfg.norm_eps, cos, sin, norm=qk_norm)
+        vn = oracle.head_norm_rope(v, None, cfg.norm_eps) if v_norm else v
+        for b in range(B):
+            ocache.k[0][b, :, p0[b]:p0[b] + T] = kn[b].float()
+            ocache.v[0][b, :, p0[b]:p0[b] + T] = vn[b].float()
+        ref = oracle.ragged_decode(qn.float(), ocache.k[0], ocache.v[0], [p + T for p in p0], window,
+                                   1.0 / math.sqrt(hd))
+        results.append((seen["z"].float().cpu(), ref.transpose(1, 2), a.last_path))
+        cache.advance(T)
+    return results
+
+
+def _downstream_argmax_ok(got, ref, vocab=256, seed=0):
+    """Logits = y @ W (W random); the argmax must agree on every row whose reference
+    top-2 margin exceeds the Cauchy-Schwarz bound on the logit error. Returns the
+    fraction of rows that were decided that way."""
+    g = torch.Generator().manual_seed(seed)
+    Bt = got.shape[0] * got.shape[1]
+    yg, yr = got.reshape(Bt, -1).double(), ref.reshape(Bt, -1).double()
+    W = torch.randn(yg.shape[1], vocab, generator=g, dtype=torch.float64) / math.sqrt(yg.shape[1])
+    lg, lr = yg @ W, yr @ W
+    bound = (yg - yr).norm(dim=1) * W.norm(dim=0).max()
+    top2 = lr.topk(2, dim=1).values
+    decided = (top2[:, 0] - top2[:, 1]) > 2 * bound
+    assert torch.equal(lg.argmax(1)[decided], lr.argmax(1)[decided])
+    return decided.double().mean().item()
+
+
+def test_config1_fp32_prefill_then_64_decode_steps():
+    """C1: fp32, batch 1, 8 q / 4 kv heads, hd 32, prefill 256 then 64 decode steps,
+    QK-norm (unit gain), theta 1e4: max-abs <= 1e-4 on every step."""
+    res = _run_layer(torch.float32, 256, 8, 4, 32, 1e4, [256] + [1] * 64, qk_norm=True)
+    for got, ref, path in res:
+        assert path == "hip-decode"
+        assert max_abs(got, ref) <= 1e-4
+
+
+def test_config2_bf16_decode():
+    """C2 shape: bf16, batch 16, 12 q / 4 kv, hd 64, cache at 2048, decode steps."""
+    res = _run_layer(torch.bfloat16, 768, 12, 4, 64, 1e4, [1] * 4, B=16, pos_start=2048)
+    for got, ref, path in res:
+        assert path == "hip-decode" and max_abs(got, ref) <= 2e-2
+        assert _downstream_argmax_ok(got, ref) >= 0.5
+
+
+def test_config3_bf16_prefill_and_decode():
+    """C3 shape: bf16, 16 q / 8 kv, hd 128, theta 1e6, gains ~N(1, 0.1): prefill of
+    1024 tokens (batch 2) through the MFMA kernel, then decode steps."""
+    res = _run_layer(torch.bfloat16, 1024, 16, 8, 128, 1e6, [1024, 1, 1], B=2)
+    assert [r[2] for r in res] == ["hip-prefill", "hip-decode", "hip-decode"]
+    for got, ref, _ in res:
+        assert max_abs(got, ref) <= 2e-2
+        assert _downstream_argmax_ok(got, ref) >= 0.5
+
+
+def test_config4_ragged_decode():
+    """C4 shape at reduced size: per-row lengths, one new token per row."""
+    lens = [1024, 3000, 1500, 4096, 1025, 2222, 3333, 1800]
+    res = _run_layer(torch.bfloat16, 1024, 16, 8, 128, 1e6, [1, 1], B=8, lens=lens)
+    for got, ref, path in res:
+        assert path == "hip-decode" and max_abs(got, ref) <= 2e-2
+        assert _downstream_argmax_ok(got, ref) >= 0.5
+
+
+@pytest.mark.parametrize("window", [1024, 0])
+def test_config5_mtp_verify(window):
+    """C5: bf16, batch 8, k=4 draft tokens verified causally over an 8192 cache, MQA 8 q /
+    1 kv, hd 256, theta 1e6; sliding-window (1024) and global layers."""
+    res = _run_layer(torch.bfloat16, 2048, 8, 1, 256, 1e6, [4, 4], B=8, window=window, pos_start=8192)
+    for got, ref, path in res:
+        assert path == "hip-decode" and max_abs(got, ref) <= 2e-2
+        assert _downstream_argmax_ok(got, ref) >= 0.5
+
+
+def test_v_norm_and_no_qk_norm():
+    res = _run_layer(torch.bfloat16, 512, 8, 2, 64, 1e4, [40, 1, 3], B=2, qk_norm=False, v_norm=True)
+    for got, ref, _ in res:
+        assert max_abs(got, ref) <= 2e-2
+
+
+# ----------------------------------------------------------------------------- callers
+def _tiny(**kw):
+    from sleuth_amd.config import ModelConfig
+    from sleuth_amd.model import Transformer
+
+    torch.manual_seed(0)
+    cfg = dict(vocab_size=200, d_model=128, n_layers=3, n_heads=4, n_kv_heads=2, max_seq_len=160,
+               qk_norm=True)
+    cfg.update(kw)
+    return Transformer(ModelConfig(**cfg)).eval()
+
+
+def test_kv_cache_matches_full_forward_fp32():
+    """tests/test_model.py:61-69 through the HIP path (fp32)."""
+    from sleuth_amd.kv_cache import KVCache
+
+    m = _tiny(layer_types=["sliding", "full", "sliding"], sliding_window=6).to(DEV)
+    x = torch.randint(0, 200, (2, 40), device=DEV)
+    with torch.no_grad():
+        full = m(x).logits
+        cache = KVCache.for_model(m, batch=2)
+        parts = [m(x[:, :20], cache=cache).logits, m(x[:, 20:25], cache=cache).logits]
+        parts += [m(x[:, i:i + 1], cache=cache).logits for i in range(25, 40)]
+    assert m.blocks[0].attn.last_path == "hip-decode"
+    assert max_abs(torch.cat(parts, 1), full) <= 1e-4
+
+
+def test_bf16_kv_cache_close_to_full_forward():
+    """tests/test_gpu.py:38-49 (bf16 cache vs full forward, loose)."""
+    from sleuth_amd.kv_cache import KVCache
+
+    m = _tiny().to(DEV, torch.bfloat16)
+    x = torch.randint(0, 200, (1, 48), device=DEV)
+    with torch.no_grad():
+        full = m(x).logits.float()
+        cache = KVCache.for_model(m, 1)
+        parts = [m(x[:, :32], cache=cache).logits.float()]
+        parts += [m(x[:, i:i + 1], cache=cache).logits.float() for i in range(32, 48)]
+    assert m.blocks[1].attn.last_path == "hip-decode"
+    assert (torch.cat(parts, 1) - full).abs().max().item() < 0.1
+
+
+def test_graph_generation_matches_eager():
+    """tests/test_cuda_graph.py:64-78: greedy tokens with HIP graphs = without, across
+    two length buckets, and the graphs are reused by the next call."""
+    from sleuth_amd.generate import generate
+
+    m = _tiny(layer_types=["sliding", "full", "sliding"], sliding_window=8, max_seq_len=96).to(DEV, torch.bfloat16)
+    prompt = [1, 5, 9, 13]
+    eager = generate(m, prompt, 80)
+    graph = generate(m, prompt, 80, cuda_graph=True)
+    assert graph.new_ids == eager.new_ids
+    assert graph.stats["graphs"] == [64, 96]
+    again = generate(m, prompt, 80, cuda_graph=True)
+    assert again.new_ids == eager.new_ids
+
+
+@pytest.mark.parametrize("cuda_graph", [False, True])
+def test_speculative_matches_plain(cuda_graph):
+    """tests/test_speculative.py:31-45, 81-94: greedy speculative == plain greedy, k = 4,
+    sliding + full layers, up to the end of the context."""
+    from sleuth_amd.generate import generate, speculative_generate
+
+    m = _tiny(layer_types=["sliding", "full"], n_layers=2, sliding_window=8, max_seq_len=96).to(DEV, torch.bfloat16)
+    prompt = [1, 5, 9, 13, 5, 9, 13, 5, 9, 13, 22, 5, 9]
+    plain = generate(m, prompt, 83)
+    spec = speculative_generate(m, prompt, 83, k=4, cuda_graph=cuda_graph)
+    assert spec.new_ids == plain.new_ids
+    s = spec.stats["speculative"]
+    assert s["forwards"] < len(spec.new_ids)
+
+
+def test_taps_on_the_hip_path():
+    """Listening on attn.q / attn.k keeps the HIP path (materialised q/k) and the same
+    result; attn.pattern forces the torch path; zeroing attn.z ablates the heads."""
+    from sleuth_amd.taps import listen
+
+    m = _tiny(d_model=256).to(DEV, torch.bfloat16)   # head dim 64: the MFMA prefill
+    x = torch.randint(0, 200, (1, 24), device=DEV)
+    with torch.no_grad():
+        base = m(x).logits.float()
+        assert m.blocks[0].attn.last_path == "hip-prefill"
+        seen = {}
+        with listen(m, {"blocks.0.attn.q": lambda n, t: seen.setdefault("q", t),
+                        "blocks.0.attn.k": lambda n, t: seen.setdefault("k", t)}):
+            tapped = m(x).logits.float()
+        assert m.blocks[0].attn.last_path == "hip-prefill"
+        assert seen["q"].shape == (1, 4, 24, 64) and seen["k"].shape == (1, 2, 24, 64)
+        assert (tapped - base).abs().max().item() < 2e-2
+        with listen(m, {"blocks.*.attn.pattern": lambda n, t: None}):
+            m(x)
+        assert m.blocks[0].attn.last_path == "torch"
+        with listen(m, {"blocks.*.attn.z": lambda n, t: torch.zeros_like(t)}):
+            ablated = m(x).logits.float()
+        assert not torch.allclose(base, ablated)
+
+
+def test_static_step_equals_normal_step_on_gpu():
+    """A static (graph-ready) step of 5 tokens == the normal path (tests/test_cuda_graph.py:81-95)."""
+    from sleuth_amd.kv_cache import StaticKVCache
+
+    m = _tiny(layer_types=["sliding", "full", "sliding"], sliding_window=8).to(DEV)
+    ids = torch.randint(0, 200, (1, 30), device=DEV)
+    shapes = [(m.cfg.attn_spec(i).kv_heads, m.cfg.attn_spec(i).head_dim) for i in range(m.cfg.n_layers)]
+    with torch.no_grad():
+        full = m(ids).logits[0]
+        st = StaticKVCache(shapes, 1, 96, DEV, torch.float32, tokens_per_step=5)
+        m(ids[:, :20], cache=st)
+        st.length, st.static = 32, True
+        st.pos_t.fill_(20)
+        out = m(ids[:, 20:25], cache=st).logits[0]
+        st.static = False
+    assert max_abs(out, full[20:25]) <= 1e-4

@@ -1,0 +1,221 @@
+"""Host logic of the drop-in module, cache and callers on the CPU (torch path): the same
+behaviour the reference's CPU tests assert (tests/test_model.py, test_cuda_graph.py,
+test_speculative.py), checked against the oracle."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from sleuth_amd.attention import Attention
+from sleuth_amd.config import ModelConfig
+from sleuth_amd.generate import generate, ngram_draft, speculative_generate
+from sleuth_amd.kv_cache import KVCache, StaticKVCache
+from sleuth_amd.model import Transformer
+from sleuth_amd.taps import assign_tap_names, listen, tap_names
+
+VARIANTS = [
+    dict(),
+    dict(n_kv_heads=2, qk_norm=True),
+    dict(n_kv_heads=1),
+    dict(layer_types=["sliding", "full", "sliding"], sliding_window=5, head_size=32, n_kv_heads=1,
+         swa_head_size=16, swa_kv_heads=2, swa_rope_theta=100.0, full_v_from_k=True, qk_norm=True,
+         v_norm=True, attn_scale=1.0),
+    dict(pos_type="none"),
+]
+
+
+def make(**kw):
+    torch.manual_seed(0)
+    cfg = ModelConfig(**{"vocab_size": 300, "d_model": 64, "n_layers": 3, "n_heads": 4, "max_seq_len": 48, **kw})
+    return Transformer(cfg).eval()
+
+
+def test_attention_signature_and_names():
+    cfg = ModelConfig(vocab_size=10, d_model=64, n_heads=4, n_kv_heads=2, qk_norm=True)
+    a = Attention(cfg, 0)
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm", "tap_q", "tap_k",
+                 "tap_pattern", "tap_z"):
+        assert hasattr(a, name), name
+    x = torch.randn(2, 5, 64)
+    cos, sin = oracle.rope_tables(16, 5, 1e4)
+    assert a(x, cos, sin).shape == (2, 5, 64)
+    assert a.last_path == "torch"
+
+
+@pytest.mark.parametrize("qk_norm,v_norm,window", [(True, False, 0), (True, True, 3), (False, False, 0)])
+def test_module_torch_path_matches_oracle(qk_norm, v_norm, window):
+    cfg = ModelConfig(vocab_size=10, d_model=64, n_heads=4, n_kv_heads=2, qk_norm=qk_norm, v_norm=v_norm,
+                      layer_types=["sliding"] if window else [], sliding_window=window, n_layers=1)
+    torch.manual_seed(1)
+    a = Attention(cfg, 0).eval()
+    if qk_norm:
+        with torch.no_grad():
+            a.q_norm.weight.add_(0.1 * torch.randn(16))
+            a.k_norm.weight.add_(0.1 * torch.randn(16))
+    x = torch.randn(2, 7, 64)
+    cos, sin = oracle.rope_tables(16, 7, 1e4)
+    seen = {}
+    assign_tap_names(a)
+    with torch.no_grad(), listen(a, {"z": lambda n, t: seen.setdefault("z", t)}):
+        a(x, cos, sin)
+        q = a.q_proj(x).view(2, 7, 4, 16).transpose(1, 2)
+        k = a.k_proj(x).view(2, 7, 2, 16).transpose(1, 2)
+        v = a.v_proj(x).view(2, 7, 2, 16).transpose(1, 2)
+        want = oracle.attention_forward(q, k, v, cos=cos, sin=sin, scale=0.25, eps=cfg.norm_eps,
+                                        q_weight=a.q_norm.weight if qk_norm else None,
+                                        k_weight=a.k_norm.weight if qk_norm else None, qk_norm=qk_norm,
+                                        v_norm=v_norm, window=window, fused_norm=False)
+    torch.testing.assert_close(seen["z"], want.transpose(1, 2), atol=1e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("kw", VARIANTS)
+def test_explicit_attention_matches_fused(kw):
+    """tests/test_model.py:51-58"""
+    m = make(**kw)
+    x = torch.randint(0, 300, (2, 20))
+    with torch.no_grad():
+        fused = m(x).logits
+        with listen(m, {"blocks.*.attn.pattern": lambda name, t: None}):
+            explicit = m(x).logits
+    torch.testing.assert_close(fused, explicit, atol=1e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("kw", VARIANTS)
+def test_kv_cache_matches_full_forward(kw):
+    """tests/test_model.py:61-69: chunked prefill + token by token == one pass."""
+    m = make(**kw)
+    x = torch.randint(0, 300, (2, 24))
+    with torch.no_grad():
+        full = m(x).logits
+        cache = KVCache.for_model(m, batch=2)
+        parts = [m(x[:, :9], cache=cache).logits, m(x[:, 9:15], cache=cache).logits]
+        parts += [m(x[:, i:i + 1], cache=cache).logits for i in range(15, 24)]
+    torch.testing.assert_close(torch.cat(parts, 1), full, atol=1e-5, rtol=1e-4)
+
+
+def test_ragged_cache_rows_match_single_rows():
+    """Per-row lengths: each row of a ragged batch decodes like that row alone."""
+    m = make(n_kv_heads=2, qk_norm=True)
+    ids = torch.randint(0, 300, (3, 20))
+    lens = [4, 11, 7]
+    with torch.no_grad():
+        cache = KVCache.for_model(m, batch=3)
+        singles = []
+        for b, L in enumerate(lens):
+            c1 = KVCache.for_model(m, batch=1)
+            m(ids[b:b + 1, :L], cache=c1)
+            singles.append((c1, m(ids[b:b + 1, L:L + 1], cache=c1).logits))
+            for layer in range(m.cfg.n_layers):
+                cache.k[layer][b:b + 1, :, :L] = c1.k[layer][:, :, :L]
+                cache.v[layer][b:b + 1, :, :L] = c1.v[layer][:, :, :L]
+        cache.set_lengths(lens)
+        step = torch.stack([ids[b, L] for b, L in enumerate(lens)])[:, None]
+        out = m(step, cache=cache).logits
+    for b in range(3):
+        torch.testing.assert_close(out[b:b + 1], singles[b][1], atol=1e-5, rtol=1e-4)
+    assert cache.seq_lens_host == [5, 12, 8] and cache.seq_lens.tolist() == [5, 12, 8]
+
+
+def test_cache_protocol():
+    c = KVCache([(2, 8), (1, 16)], 2, 10, "cpu", torch.float32)
+    assert c.k[0].shape == (2, 2, 10, 8) and c.k[1].shape == (2, 1, 10, 16) and c.pos == 0
+    assert c.nbytes() == 2 * 4 * (2 * 2 * 10 * 8 + 2 * 1 * 10 * 16)
+    k = torch.randn(2, 2, 3, 8)
+    ka, va = c.update(0, k, k)
+    assert ka.shape == (2, 2, 3, 8) and torch.equal(ka, k)
+    c.advance(3)
+    with pytest.raises(ValueError, match="KV cache full"):
+        c.update(0, torch.randn(2, 2, 8, 8), torch.randn(2, 2, 8, 8))
+    with pytest.raises(ValueError, match="KV cache full"):
+        c.check_room(8)
+    h = c.token_history(2, "cpu")
+    assert h.shape == (2, 10) and torch.all(h == -1)
+    c.reset()
+    assert c.pos == 0
+
+
+def test_static_cache_masks_and_positions():
+    """tests/test_cuda_graph.py:55-61 golden masks, on the product cache."""
+    c = StaticKVCache([(1, 4)], 1, 32, "cpu", torch.float32)
+    c.length, c.static = 16, True
+    c.pos_t.fill_(10)
+    assert c.attn_mask().view(-1).tolist() == [True] * 11 + [False] * 5
+    assert c.attn_mask(4).view(-1).nonzero().view(-1).tolist() == [7, 8, 9, 10]
+    c2 = StaticKVCache([(1, 4)], 1, 32, "cpu", torch.float32, tokens_per_step=3)
+    c2.pos_t.fill_(5)
+    assert c2.positions.tolist() == [5, 6, 7]
+
+
+@pytest.mark.parametrize("kw", [{}, {"layer_types": ["sliding", "full", "sliding"], "sliding_window": 8}])
+def test_static_decode_matches_normal_decode(kw):
+    """tests/test_cuda_graph.py:24-52 (static steps on the CPU, two length buckets)."""
+    m = make(n_kv_heads=2, max_seq_len=96, **kw)
+    ids = torch.randint(0, 300, (1, 40))
+    shapes = [(m.cfg.attn_spec(i).kv_heads, m.cfg.attn_spec(i).head_dim) for i in range(m.cfg.n_layers)]
+    normal = KVCache(shapes, 1, 96, "cpu", torch.float32)
+    static = StaticKVCache(shapes, 1, 96, "cpu", torch.float32)
+    with torch.no_grad():
+        a = m(ids[:, :5], cache=normal).logits[:, -1]
+        b = m(ids[:, :5], cache=static).logits[:, -1]
+        assert torch.allclose(a, b, atol=1e-5)
+        for t in ids[0, 5:]:
+            tok = t.view(1, 1)
+            a = m(tok, cache=normal).logits[:, -1]
+            pos = static.pos
+            static.length = 16 if pos < 16 else 64
+            static.pos_t.fill_(pos)
+            static.static = True
+            b = m(tok, cache=static).logits[:, -1]
+            static.static = False
+            static.pos += 1
+            assert torch.allclose(a, b, atol=1e-4), pos
+
+
+def test_greedy_speculative_matches_plain():
+    """tests/test_speculative.py:31-54 (prompt lookup, and a drafter that is always wrong)."""
+    m = make(n_kv_heads=2, layer_types=["sliding", "full", "sliding"], sliding_window=8, max_seq_len=128)
+    prompt = [1, 5, 9, 13, 5, 9, 13, 5, 9, 13, 22, 5, 9]
+    plain = generate(m, prompt, 40)
+    spec = speculative_generate(m, prompt, 40, k=4)
+    assert spec.new_ids == plain.new_ids
+    bad = speculative_generate(m, prompt, 40, k=3, draft=lambda ids, k: [7] * k)
+    assert bad.new_ids == plain.new_ids
+
+
+def test_ngram_draft():
+    d = ngram_draft(max_ngram=3)
+    assert d([1, 2, 3, 4, 5, 1, 2, 3], 3) == [4, 5, 1]
+    assert d([7, 8, 9, 7, 8], 2) == [9, 7]
+    assert d([1, 2, 3], 4) == []
+
+
+def test_taps_and_ablation():
+    m = make()
+    names = tap_names(m)
+    for expected in ("blocks.1.attn.z", "blocks.0.attn.q", "blocks.2.attn.pattern"):
+        assert expected in names
+    x = torch.randint(0, 300, (1, 8))
+    with torch.no_grad():
+        base = m(x).logits
+        with listen(m, {"blocks.*.attn.z": lambda n, t: torch.zeros_like(t)}):
+            ablated = m(x).logits
+        assert not torch.allclose(base, ablated)
+        torch.testing.assert_close(m(x).logits, base)
+
+
+def test_too_long_and_bad_configs_rejected():
+    m = make()
+    with pytest.raises(ValueError):
+        m(torch.zeros(1, 49, dtype=torch.long))
+    with pytest.raises(ValueError):
+        ModelConfig(vocab_size=10, d_model=64, n_heads=4, n_kv_heads=3)
+    with pytest.raises(ValueError):
+        ModelConfig(vocab_size=10, d_model=64, n_heads=4, layer_types=["sliding"] * 6)
+
+
+def test_hip_gate_on_cpu():
+    cfg = ModelConfig(vocab_size=10, d_model=64, n_heads=4)
+    a = Attention(cfg, 0)
+    assert not a._use_hip(torch.zeros(1, 4, 1, 16), None, None)
