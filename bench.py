@@ -174,14 +174,19 @@ def time_loop(fn, steps: int, warmup: int) -> float:
 
 
 def read_traffic(name: str):
-    """HBM traffic per launch measured with rocprofv3 --pmc (profiles/<name>.json), or None."""
-    p = ROOT / "profiles" / f"{name}.json"
+    """HBM bytes per launch of a kernel, measured with rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE, scaled by a copy kernel of known size) and recorded in the text summary
+    profiles/<name>.txt as a line `hbm_bytes_per_launch: N`; None if not measured."""
+    p = ROOT / "profiles" / f"{name}.txt"
     if not p.exists():
         return None
-    try:
-        return json.loads(p.read_text()).get("hbm_bytes_per_launch")
-    except (ValueError, OSError):
-        return None
+    for line in p.read_text().splitlines():
+        if line.startswith("hbm_bytes_per_launch:"):
+            try:
+                return int(float(line.split(":", 1)[1]))
+            except ValueError:
+                return None
+    return None
 
 
 # ----------------------------------------------------------------------------- CPU baseline
@@ -264,7 +269,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--extra", action="store_true", help="also print lines for configs C2, C3-decode, C5")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--only", choices=["decode", "prefill"], help="time one workload (for profiling)")
+    ap.add_argument("--only", choices=["decode", "prefill", "copy"],
+                    help="time one workload (for rocprofv3 runs); copy = a 1 GiB torch copy, the "
+                         "known-size kernel that calibrates the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the attention hot path runs on a single MI355X here "
@@ -357,10 +364,17 @@ def run_only(args, dev) -> int:
         t = time_loop(wl.step, args.steps, args.warmup)
         print(json.dumps({"workload": "C4 decode step", "us": round(t * 1e6, 2),
                           "GBs": round(wl.step_bytes() / t / 1e9, 1)}), flush=True)
-    else:
+    elif args.only == "prefill":
         pf = PrefillWorkload(4, 4096, 16, 8, 128, 1e6, torch.bfloat16, dev)
         t = time_loop(pf.step, args.steps, args.warmup)
         print(json.dumps({"workload": "C3 prefill step", "us": round(t * 1e6, 2)}), flush=True)
+    else:
+        n = 1 << 30
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        t = time_loop(lambda: dst.copy_(src), args.steps, args.warmup)
+        print(json.dumps({"workload": "copy 1 GiB", "bytes_read": n, "bytes_written": n, "us": round(t * 1e6, 2),
+                          "GBs": round(2 * n / t / 1e9, 1)}), flush=True)
     return 0
 
 
