@@ -42,6 +42,14 @@ __device__ __forceinline__ uint4 load16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
+// 8 consecutive fp32 values from a 16-byte aligned address, as two 16-byte loads.
+__device__ __forceinline__ void load_f32x8(const float* p, float* out) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+  out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+}
+
 __device__ __forceinline__ void store16(void* p, const uint4& v) {
   *reinterpret_cast<uint4*>(p) = v;
 }

@@ -1,24 +1,31 @@
 // Causal prefill on bf16/fp16 MFMA (gfx950 v_mfma_f32_32x32x16_{bf16,f16}).
 //
-// A block of 4 waves owns BM = 128 queries of one (b, head); each wave owns 32 of them.
-// K and V tiles of BN = 64 keys are staged in LDS (the next tile is prefetched into
-// registers while the current one is used) and shared by the 4 waves.
+// A block of 4 waves owns BM = 128 queries of one (b, head); each wave owns 32 of them
+// and keeps them for the whole block, together with its output accumulator. Key tiles
+// of BN keys (64 for head dim <= 128, 32 for 256) stream through LDS:
 //
-// Scores are computed transposed, S^T = K . Q^T, with K as the MFMA A operand (read
-// row-major from LDS) and Q^T as the B operand (held in registers for the whole block).
-// In the 32x32 accumulator layout every lane then owns ONE query (column l % 32) and 16
-// of the 32 keys of a block (rows 8i + 4(l/32) + j), so the online softmax needs one
-// cross-lane step per reduction (lane l <-> l ^ 32), and the output accumulator
-// O^T = V^T . P^T has the same property: all 16 values of a lane belong to its query,
-// so the rescale by exp(m_old - m_new) is a per-lane scalar.
+//   * K and V tiles go from HBM straight into LDS with global_load_lds_dwordx4 (no
+//     staging registers, no VALU). Each lane's 16 bytes land at LDS slot `lane`, so the
+//     16-byte chunk a lane fetches decides the LDS layout: chunk c of key row r is stored
+//     at chunk position c ^ swz(r), an XOR swizzle that keeps the MFMA operand reads
+//     below free of bank conflicts. Two LDS stages: the loads of tile j+1 are issued
+//     before tile j is computed, and one barrier per tile separates the stages.
+//   * Scores are computed transposed, S^T = K . Q^T: K is the MFMA A operand (128-bit
+//     LDS reads), Q^T the B operand held in registers for the whole block. In the 32x32
+//     accumulator layout each lane then owns ONE query (column l % 32) and 16 keys of a
+//     32-key block (rows 8i + 4(l/32) + j), so the online softmax of a query needs a
+//     single cross-lane exchange per tile (lane l <-> l ^ 32) for the running max, and
+//     none for the running sum (the two halves are added once at the end).
+//   * P^T is fed to the second MFMA (O^T = V^T . P^T) straight from the score registers:
+//     MFMA k index 8hi + 4i' + j stands for key 16*half + 8i' + 4hi + j, exactly the keys
+//     the lane already holds. The matching V^T operand is read from the row-major V tile
+//     with ds_read_b64_tr_b16 (gfx950's transposing LDS read: within each 16-lane group,
+//     lane i receives element i % 4 of the 4-element rows addressed by lanes 4k + i / 4,
+//     k = 0..3), two reads of 4 keys per MFMA.
+//   * The running max only moves when a score exceeds it by 2^8 (log2 units), so the
+//     rescale of the accumulator is rare; weights stay <= 2^8, safe in bf16/fp16.
 //
-// P^T is fed to the second MFMA straight from the score registers: lane (n, hi) holds
-// keys {8i + 4hi + j}; the MFMA's k index 8hi + 4i' + j is mapped to key
-// 16*half + 8i' + 4hi + j (i = 2*half + i'). V is written to LDS transposed (V^T, one
-// row per head-dim channel) with its key columns permuted the same way, so each lane
-// reads its 8 keys of V^T with one 128-bit LDS load.
-//
-// Q gets the per-head RMSNorm and RoPE in the load (fp32 math, one rounding), like
+// Q gets the per-head RMSNorm and RoPE in its load (fp32 math, one rounding), like
 // fused_ops._head_kernel (fused_ops.py:53-85); K and V come from the cache, where
 // forge_kv_append wrote them already normalised.
 #include "common.h"
@@ -28,7 +35,9 @@ namespace forge {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16> {
@@ -58,56 +67,82 @@ struct PrefillParams {
   int64_t skb, skh, sks;
   int64_t offset;
   int B, T, H, K, G;
-  int nqt;  // query tiles
+  int nqt;       // query tiles per (b, head)
+  int xcd_map;   // 1: blocks of one (b, kv head) pair run on one XCD (B*K % 8 == 0)
   int window;
   float scale_log2;
   void* out;
   int64_t sob, sot, soh;
 };
 
-constexpr int kBM = 128;
-constexpr int kBN = 64;
-constexpr int kPad = 8;  // elements of padding per LDS row
+constexpr int kWaves = 4;
+constexpr int kBM = 32 * kWaves;
+constexpr float kLazyLog2 = 8.0f;
 
-// Column of key k (0..63 within a tile) in the permuted V^T rows.
-__device__ __forceinline__ int vt_col(int k) {
-  const int kb = k >> 5, kk = k & 31;
-  const int half = kk >> 4, k16 = kk & 15;
-  const int ip = k16 >> 3, hi = (k16 & 7) >> 2, j = k16 & 3;
-  return kb * 32 + half * 16 + hi * 8 + ip * 4 + j;
+template <int D> struct Tile {
+  static constexpr int BN = D >= 256 ? 32 : 64;       // keys per tile
+  static constexpr int NCH = D / 8;                    // 16-byte chunks per key row
+  static constexpr int ROWB = 2 * D;                   // bytes per key row
+  static constexpr int TILEB = BN * ROWB;              // bytes of one K (or V) tile
+  static constexpr int LOADS = TILEB / (kWaves * 1024);  // 16-byte loads per lane per tile
+  static_assert(LOADS * kWaves * 1024 == TILEB, "tile must split into whole wave loads");
+};
+
+// XOR swizzles of the 16-byte chunk index by key row (see the reads below).
+template <int D> __device__ __forceinline__ int swz_k(int row) {
+  return row & ((D / 8 >= 16 ? 16 : D / 8) - 1);
+}
+template <int D> __device__ __forceinline__ int swz_v(int row) {
+  return D / 8 >= 16 ? (row & 3) << 2 : ((row >> 1) & 1) << 2;
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
-  using V8 = typename Mfma<T>::vec;
-  constexpr int KSTEPS = D / 16;  // MFMA k-steps over the head dim (scores)
-  constexpr int DB = D / 32;      // 32-channel blocks of the output
-  constexpr int KCH = D / 8;      // 16-byte chunks per K/V row
-  constexpr int KTOTAL = kBN * KCH;        // 16-byte K chunks per tile
-  constexpr int VTOTAL = (kBN / 4) * KCH;  // V pieces of 4 keys x 8 channels per tile
-  constexpr int KLOADS = (KTOTAL + 255) / 256;
-  constexpr int VQUADS = (VTOTAL + 255) / 256;
+__device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-  __shared__ __attribute__((aligned(16))) T sK[kBN][D + kPad];
-  __shared__ __attribute__((aligned(16))) T sVt[D][kBN + kPad];
+template <typename T, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2)))
+void prefill_kernel(PrefillParams p) {
+  using V8 = typename Mfma<T>::vec;
+  using TL = Tile<D>;
+  constexpr int BN = TL::BN;
+  constexpr int KB = BN / 32;       // 32-key blocks per tile
+  constexpr int KSTEPS = D / 16;    // MFMA k-steps over the head dim (scores)
+  constexpr int DB = D / 32;        // 32-channel blocks of the output
+  constexpr int HALVES = BN / 16;   // 16-key MFMA steps of P.V
+
+  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::TILEB];  // [stage][K|V]
 
   const int tid = threadIdx.x;
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
   const int n = lane & 31;
   const int hi = lane >> 5;
 
-  // Block -> (query tile, head, batch). Heavy (late) causal tiles go first; the heads
-  // of one KV group and the batch rows are ordered so that blocks reading the same K/V
-  // are 8 apart in launch order, i.e. on the same XCD (and its L2).
-  const int HB = p.H * p.B;
-  const int qt = p.nqt - 1 - (int)(blockIdx.x / HB);
-  const int hb = blockIdx.x % HB;
-  const int P = p.B * p.K;
-  const int pair = hb % P;
-  const int gq = hb / P;
-  const int b = pair / p.K;
-  const int kvh = pair % p.K;
+  // ---- block -> (query tile, head, batch). Heavy (late) causal tiles first. With
+  // xcd_map, block i runs on XCD i % 8 and all blocks of one (b, kv head) pair share an
+  // XCD, so the K/V they all read stays in that XCD's L2.
+  int qt, b, kvh, gq;
+  {
+    const int bid = blockIdx.x;
+    const int P = p.B * p.K;
+    if (p.xcd_map) {
+      const int x = bid & 7, local = bid >> 3;
+      const int per = (P >> 3) * p.G;  // (pair, head) combinations per XCD
+      const int rank = local / per, rest = local % per;
+      qt = p.nqt - 1 - rank;
+      const int pair = (rest / p.G) * 8 + x;
+      gq = rest % p.G;
+      b = pair / p.K;
+      kvh = pair % p.K;
+    } else {
+      const int HB = p.H * p.B;
+      qt = p.nqt - 1 - bid / HB;
+      const int hb = bid % HB;
+      const int pair = hb % P;
+      gq = hb / P;
+      b = pair / p.K;
+      kvh = pair % p.K;
+    }
+  }
   const int h = kvh * p.G + gq;
 
   const int i_q = qt * kBM + wave * 32 + n;  // this lane's query (index into T)
@@ -115,7 +150,50 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
   const int64_t qpos = p.offset + i_q;
   const int64_t S = p.offset + p.T;
 
-  // ---- Q: load, fused RMSNorm + RoPE, one rounding, kept as MFMA B operands.
+  // ---- key tiles of the block, and the first stage's loads (issued before the Q math)
+  const int64_t q_first = p.offset + (int64_t)qt * kBM;
+  const int64_t q_last_idx =
+      (int64_t)qt * kBM + kBM - 1 < p.T - 1 ? (int64_t)qt * kBM + kBM - 1 : p.T - 1;
+  const int64_t blk_kmax = p.offset + q_last_idx;
+  int64_t blk_kmin = p.window > 0 ? q_first - p.window + 1 : 0;
+  if (blk_kmin < 0) blk_kmin = 0;
+  const int kt_begin = (int)(blk_kmin / BN);
+  const int kt_end = (int)(blk_kmax / BN);
+
+  const T* kg = static_cast<const T*>(p.k) + b * p.skb + kvh * p.skh;
+  const T* vg = static_cast<const T*>(p.v) + b * p.skb + kvh * p.skh;
+
+  // Per-lane source offsets of the direct loads: load n of this wave fills LDS slots
+  // (wave*LOADS + n)*64 + lane, i.e. key row slot / NCH and swizzled chunk slot % NCH.
+  int ld_row[TL::LOADS], ld_kch[TL::LOADS], ld_vch[TL::LOADS];
+#pragma unroll
+  for (int i = 0; i < TL::LOADS; ++i) {
+    const int slot = (wave * TL::LOADS + i) * 64 + lane;
+    const int row = slot / TL::NCH, pch = slot % TL::NCH;
+    ld_row[i] = row;
+    ld_kch[i] = (pch ^ swz_k<D>(row)) * 8;
+    ld_vch[i] = (pch ^ swz_v<D>(row)) * 8;
+  }
+  auto issue = [&](int kt, int stage) {
+    const int64_t key0 = (int64_t)kt * BN;
+#pragma unroll
+    for (int i = 0; i < TL::LOADS; ++i) {
+      int64_t key = key0 + ld_row[i];
+      if (key > S - 1) key = S - 1;  // rows past the end are masked; read a valid one
+      const T* ksrc = kg + key * p.sks + ld_kch[i];
+      const T* vsrc = vg + key * p.sks + ld_vch[i];
+      __builtin_amdgcn_global_load_lds((const void*)ksrc,
+                                       (lds_void*)(smem[stage][0] + (wave * TL::LOADS + i) * 1024),
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)vsrc,
+                                       (lds_void*)(smem[stage][1] + (wave * TL::LOADS + i) * 1024),
+                                       16, 0, 0);
+    }
+  };
+  if (kt_begin <= kt_end) issue(kt_begin, 0);
+
+  // ---- Q: load, fused RMSNorm + RoPE, one rounding, kept as MFMA B operands. Lane
+  // (n, hi) holds channels 16s + 8hi + e; gains and RoPE rows come in 16-byte loads.
   V8 qreg[KSTEPS];
   {
     float qf[KSTEPS][8];
@@ -140,23 +218,35 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          qf[s][e] *= rs;
-          if (p.qw) qf[s][e] *= p.qw[16 * s + 8 * hi + e];
-        }
+        for (int e = 0; e < 8; ++e) qf[s][e] *= rs;
+      if (p.qw) {
+        float w[KSTEPS][8];
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) load_f32x8(p.qw + 16 * s + 8 * hi, w[s]);
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qf[s][e] *= w[s][e];
+      }
     }
     if ((p.flags & FORGE_ROPE) && valid_q) {
       const float* cr = p.cos + (int64_t)i_q * p.cst;
       const float* sr = p.sin + (int64_t)i_q * p.cst;
 #pragma unroll
-      for (int s = 0; s < KSTEPS / 2; ++s)
+      for (int s = 0; s < KSTEPS / 2; ++s) {
+        const int x = 16 * s + 8 * hi;  // first-half channels x..x+7; partners x + D/2
+        float c1[8], s1[8], c2[8], s2[8];
+        load_f32x8(cr + x, c1);
+        load_f32x8(sr + x, s1);
+        load_f32x8(cr + x + D / 2, c2);
+        load_f32x8(sr + x + D / 2, s2);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int x = 16 * s + 8 * hi + e;  // first-half channel; partner x + D/2
           const float a = qf[s][e], z = qf[s + KSTEPS / 2][e];
-          qf[s][e] = a * cr[x] - z * sr[x];
-          qf[s + KSTEPS / 2][e] = z * cr[x + D / 2] + a * sr[x + D / 2];
+          qf[s][e] = a * c1[e] - z * s1[e];
+          qf[s + KSTEPS / 2][e] = z * c2[e] + a * s2[e];
         }
+      }
     }
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
@@ -164,74 +254,23 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
       for (int e = 0; e < 8; ++e) qreg[s][e] = from_f32<T>(qf[s][e]);
   }
 
-  // ---- key tiles this block needs
-  const int64_t q_first = p.offset + (int64_t)qt * kBM;
-  const int64_t q_last_idx = (int64_t)qt * kBM + kBM - 1 < p.T - 1 ? (int64_t)qt * kBM + kBM - 1 : p.T - 1;
-  const int64_t blk_kmax = p.offset + q_last_idx;
-  int64_t blk_kmin = p.window > 0 ? q_first - p.window + 1 : 0;
-  if (blk_kmin < 0) blk_kmin = 0;
-  const int kt_begin = (int)(blk_kmin / kBN);
-  const int kt_end = (int)(blk_kmax / kBN);
-
-  // this wave's query span (for tile skipping and the mask-free fast path)
+  // this wave's query span (tile skipping and the mask-free fast path)
   const int w_first = qt * kBM + wave * 32;
   const int w_last = w_first + 31 < p.T - 1 ? w_first + 31 : p.T - 1;
   const bool wave_any = w_first < p.T;
   const int64_t wq_lo = p.offset + w_first, wq_hi = p.offset + w_last;
 
-  const T* kg = static_cast<const T*>(p.k) + b * p.skb + kvh * p.skh;
-  const T* vg = static_cast<const T*>(p.v) + b * p.skb + kvh * p.skh;
-
-  uint4 kpre[KLOADS];
-  uint4 vpre[VQUADS][4];
-  auto prefetch = [&](int kt) {
-    const int64_t key0 = (int64_t)kt * kBN;
-#pragma unroll
-    for (int i = 0; i < KLOADS; ++i) {
-      const int idx = tid + i * 256;
-      const int r = idx / KCH, ch = idx % KCH;
-      const int64_t key = key0 + r;
-      kpre[i] = (idx < KTOTAL && key < S) ? load16(kg + key * p.sks + ch * 8) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < VQUADS; ++i) {
-      const int idx = tid + i * 256;
-      const int kq = idx / KCH, ho = idx % KCH;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t key = key0 + kq * 4 + r;
-        vpre[i][r] = (idx < VTOTAL && key < S) ? load16(vg + key * p.sks + ho * 8)
-                                               : make_uint4(0, 0, 0, 0);
-      }
-    }
-  };
-  auto commit = [&]() {
-#pragma unroll
-    for (int i = 0; i < KLOADS; ++i) {
-      const int idx = tid + i * 256;
-      if (KTOTAL % 256 && idx >= KTOTAL) break;
-      const int r = idx / KCH, ch = idx % KCH;
-      store16(&sK[r][ch * 8], kpre[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < VQUADS; ++i) {
-      const int idx = tid + i * 256;
-      if (VTOTAL % 256 && idx >= VTOTAL) break;
-      const int kq = idx / KCH, ho = idx % KCH;
-      const int col = vt_col(kq * 4);
-      const unsigned short* e0 = reinterpret_cast<const unsigned short*>(&vpre[i][0]);
-      const unsigned short* e1 = reinterpret_cast<const unsigned short*>(&vpre[i][1]);
-      const unsigned short* e2 = reinterpret_cast<const unsigned short*>(&vpre[i][2]);
-      const unsigned short* e3 = reinterpret_cast<const unsigned short*>(&vpre[i][3]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        uint2 w;
-        w.x = (unsigned)e0[e] | ((unsigned)e1[e] << 16);
-        w.y = (unsigned)e2[e] | ((unsigned)e3[e] << 16);
-        *reinterpret_cast<uint2*>(&sVt[ho * 8 + e][col]) = w;
-      }
-    }
-  };
+  // LDS read offsets (bytes within a stage buffer).
+  // K operand: row 32kb + n, chunk 2s + hi, swizzled by row & 15 == n & 15.
+  const int k_rd = n * TL::ROWB;
+  const int k_sw = swz_k<D>(n);
+  // V^T operand (tr reads): source lane role g = lane/16, kq = (lane/4)%4, qq = lane%4
+  // addresses key row 16*half + 8i' + 4(g/2) + kq, channel 32db + 16(g%2) + 4qq.
+  const int g = lane >> 4, kq = (lane >> 2) & 3, qq = lane & 3;
+  const int v_row = 4 * (g >> 1) + kq;
+  const int v_sw = swz_v<D>(v_row);  // rows differ from v_row by multiples of 8: same swizzle
+  const int v_chlo = 2 * (g & 1) + (qq >> 1);  // chunk within the 32-channel block (0..3)
+  const int v_byte = 8 * (qq & 1);
 
   floatx16 oacc[DB];
 #pragma unroll
@@ -239,85 +278,103 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
 #pragma unroll
     for (int x = 0; x < 16; ++x) oacc[d][x] = 0.0f;
   float m_run = kNegInf, l_run = 0.0f;
+  const float c = p.scale_log2;
 
-  if (kt_begin <= kt_end) prefetch(kt_begin);
   for (int kt = kt_begin; kt <= kt_end; ++kt) {
-    __syncthreads();
-    commit();
-    __syncthreads();
-    if (kt + 1 <= kt_end) prefetch(kt + 1);
+    const int stage = (kt - kt_begin) & 1;
+    wait_vm_all();
+    __syncthreads();  // tile kt is in LDS for every wave; stage^1 is free again
+    if (kt + 1 <= kt_end) issue(kt + 1, stage ^ 1);
 
-    const int64_t key0 = (int64_t)kt * kBN;
-    // Does this tile hold any key visible to this wave? (wave-uniform)
+    const int64_t key0 = (int64_t)kt * BN;
     const bool wave_needs = wave_any && key0 <= wq_hi &&
-                            (p.window <= 0 || key0 + kBN - 1 > wq_lo - p.window);
+                            (p.window <= 0 || key0 + BN - 1 > wq_lo - p.window);
     if (!wave_needs) continue;
-    const bool full = key0 + kBN - 1 <= wq_lo && key0 + kBN - 1 < S &&
+    const bool full = key0 + BN - 1 <= wq_lo && key0 + BN - 1 < S &&
                       (p.window <= 0 || wq_hi - key0 < p.window) && w_last - w_first == 31;
 
-    floatx16 sacc[2];
+    const char* kl = smem[stage][0];
+    const char* vl = smem[stage][1];
+
+    // ---- S^T = K . Q^T
+    floatx16 sacc[KB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
       for (int x = 0; x < 16; ++x) sacc[kb][x] = 0.0f;
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
-        const V8 a = *reinterpret_cast<const V8*>(&sK[kb * 32 + n][16 * s + 8 * hi]);
+        const V8 a = *reinterpret_cast<const V8*>(
+            kl + kb * 32 * TL::ROWB + k_rd + (((2 * s + hi) ^ k_sw) << 4));
         sacc[kb] = Mfma<T>::run(a, qreg[s], sacc[kb]);
       }
     }
 
+    // ---- online softmax (base 2, scale folded into the exponent)
     float mx = kNegInf;
+    if (full) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-      for (int x = 0; x < 16; ++x) {
-        float v = sacc[kb][x] * p.scale_log2;
-        if (!full) {
+        for (int x = 0; x < 16; ++x) mx = fmaxf(mx, sacc[kb][x]);
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
           const int64_t key = key0 + kb * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);
           const bool ok = valid_q && key <= qpos && key < S &&
                           (p.window <= 0 || qpos - key < p.window);
-          if (!ok) v = kNegInf;
+          if (!ok) sacc[kb][x] = kNegInf;
+          mx = fmaxf(mx, sacc[kb][x]);
         }
-        sacc[kb][x] = v;
-        mx = fmaxf(mx, v);
-      }
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = rescale(m_run, m_new);
+    const float mxc = mx * c;
+    if (mxc > m_run + kLazyLog2) {
+      const float alpha = m_run == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(m_run - mxc);
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) oacc[d][x] *= alpha;
+      m_run = mxc;
+    }
+    const float m_eff = m_run == kNegInf ? 0.0f : m_run;  // all -inf so far: weights 0
     float rsum = 0.0f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int x = 0; x < 16; ++x) {
-        const float pv = exp2_masked(sacc[kb][x], m_new);
+        const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kb][x], c, -m_eff));
         sacc[kb][x] = pv;
         rsum += pv;
       }
-    rsum += __shfl_xor(rsum, 32, kWave);
-    l_run = l_run * alpha + rsum;
-    m_run = m_new;
-#pragma unroll
-    for (int d = 0; d < DB; ++d)
-#pragma unroll
-      for (int x = 0; x < 16; ++x) oacc[d][x] *= alpha;
+    l_run += rsum;
 
+    // ---- O^T += V^T . P^T
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int hf = 0; hf < HALVES; ++hf) {
+      const int kb = hf >> 1, half = hf & 1;
+      V8 pb;
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        V8 pb;
+      for (int e = 0; e < 8; ++e) pb[e] = from_f32<T>(sacc[kb][8 * half + e]);
+      const char* vrow0 = vl + (16 * hf + v_row) * TL::ROWB + v_byte;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pb[e] = from_f32<T>(sacc[kb][8 * half + e]);
-#pragma unroll
-        for (int d = 0; d < DB; ++d) {
-          const V8 a =
-              *reinterpret_cast<const V8*>(&sVt[d * 32 + n][kb * 32 + half * 16 + hi * 8]);
-          oacc[d] = Mfma<T>::run(a, pb, oacc[d]);
-        }
+      for (int d = 0; d < DB; ++d) {
+        const int ch = ((4 * d + v_chlo) ^ v_sw) << 4;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)(vrow0 + ch));
+        const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)(vrow0 + 8 * TL::ROWB + ch));
+        typedef short i16x8 __attribute__((ext_vector_type(8)));
+        const i16x8 av = __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[d] = Mfma<T>::run(__builtin_bit_cast(V8, av), pb, oacc[d]);
       }
+    }
   }
 
+  l_run += __shfl_xor(l_run, 32, kWave);
   if (!valid_q) return;
   const float inv_l = 1.0f / l_run;
   T* dst = static_cast<T*>(p.out) + b * p.sob + (int64_t)i_q * p.sot + h * p.soh;
@@ -371,6 +428,8 @@ extern "C" int forge_attn_prefill(int dtype, int B, int T, int H, int K, int D, 
   if ((sqb | sqh | sqt | skb | skh | sks) % 8)
     return set_error("forge_attn_prefill: q/k/v strides must be multiples of 8 elements");
   if ((sob | sot | soh) % 4) return set_error("forge_attn_prefill: out strides must be multiples of 4");
+  if (((uintptr_t)q_weight | (uintptr_t)cos | (uintptr_t)sin) % 16 || (cos && s_cos_t % 4))
+    return set_error("forge_attn_prefill: gain and RoPE rows must be 16-byte aligned");
   PrefillParams p{};
   p.q = q;
   p.sqb = sqb;
@@ -394,6 +453,7 @@ extern "C" int forge_attn_prefill(int dtype, int B, int T, int H, int K, int D, 
   p.K = K;
   p.G = H / K;
   p.nqt = (T + kBM - 1) / kBM;
+  p.xcd_map = (B * K) % 8 == 0 ? 1 : 0;
   p.window = window;
   p.scale_log2 = scale * kLog2e;
   p.out = out;
