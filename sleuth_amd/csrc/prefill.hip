@@ -8,8 +8,10 @@
 //     staging registers, no VALU). Each lane's 16 bytes land at LDS slot `lane`, so the
 //     16-byte chunk a lane fetches decides the LDS layout: chunk c of key row r is stored
 //     at chunk position c ^ swz(r), an XOR swizzle that keeps the MFMA operand reads
-//     below free of bank conflicts. Two LDS stages: the loads of tile j+1 are issued
-//     before tile j is computed, and one barrier per tile separates the stages.
+//     below free of bank conflicts. LDS stages (two for every head dim today): the loads
+//     of tile j+1 are issued before tile j is computed, one barrier per tile separates
+//     the stages, and two blocks share a CU so that its SIMDs interleave two independent
+//     waves.
 //   * Scores are computed transposed, S^T = K . Q^T: K is the MFMA A operand (128-bit
 //     LDS reads), Q^T the B operand held in registers for the whole block. In the 32x32
 //     accumulator layout each lane then owns ONE query (column l % 32) and 16 keys of a
@@ -75,17 +77,21 @@ struct PrefillParams {
   int64_t sob, sot, soh;
 };
 
-constexpr int kWaves = 4;
-constexpr int kBM = 32 * kWaves;
 constexpr float kLazyLog2 = 8.0f;
 
+// Block shape per head dim: WAVES waves of 32 queries each, STAGES LDS stages of one K
+// and one V tile of BN keys (loads run STAGES - 1 tiles ahead of the compute).
 template <int D> struct Tile {
-  static constexpr int BN = D >= 256 ? 32 : 64;       // keys per tile
+  static constexpr int WAVES = 4;
+  static constexpr int STAGES = 2;
+  static constexpr int BM = 32 * WAVES;                // queries per block
+  static constexpr int BN = D >= 256 ? 32 : 64;        // keys per tile
   static constexpr int NCH = D / 8;                    // 16-byte chunks per key row
   static constexpr int ROWB = 2 * D;                   // bytes per key row
   static constexpr int TILEB = BN * ROWB;              // bytes of one K (or V) tile
-  static constexpr int LOADS = TILEB / (kWaves * 1024);  // 16-byte loads per lane per tile
-  static_assert(LOADS * kWaves * 1024 == TILEB, "tile must split into whole wave loads");
+  static constexpr int LOADS = TILEB / (WAVES * 1024);   // 16-byte loads per lane per tile
+  static constexpr int LDS_BYTES = STAGES * 2 * TILEB;
+  static_assert(LOADS * WAVES * 1024 == TILEB, "tile must split into whole wave loads");
 };
 
 // XOR swizzles of the 16-byte chunk index by key row (see the reads below).
@@ -96,20 +102,29 @@ template <int D> __device__ __forceinline__ int swz_v(int row) {
   return D / 8 >= 16 ? (row & 3) << 2 : ((row >> 1) & 1) << 2;
 }
 
-__device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait until at most N vector-memory loads of this wave are outstanding (loads retire in
+// issue order, so everything issued before the last N has landed).
+template <int N> __device__ __forceinline__ void wait_vm() {
+  static_assert(N == 0 || N == 2 || N == 4 || N == 8, "add the count");
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+}
 
 template <typename T, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2)))
+__global__ __launch_bounds__(Tile<D>::WAVES * 64) __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2)))
 void prefill_kernel(PrefillParams p) {
   using V8 = typename Mfma<T>::vec;
   using TL = Tile<D>;
   constexpr int BN = TL::BN;
+  constexpr int kBM = TL::BM;
   constexpr int KB = BN / 32;       // 32-key blocks per tile
   constexpr int KSTEPS = D / 16;    // MFMA k-steps over the head dim (scores)
   constexpr int DB = D / 32;        // 32-channel blocks of the output
   constexpr int HALVES = BN / 16;   // 16-key MFMA steps of P.V
 
-  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::TILEB];  // [stage][K|V]
+  extern __shared__ __attribute__((aligned(1024))) char smem[];  // [stage][K|V][TILEB]
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -163,34 +178,52 @@ void prefill_kernel(PrefillParams p) {
   const T* kg = static_cast<const T*>(p.k) + b * p.skb + kvh * p.skh;
   const T* vg = static_cast<const T*>(p.v) + b * p.skb + kvh * p.skh;
 
-  // Per-lane source offsets of the direct loads: load n of this wave fills LDS slots
-  // (wave*LOADS + n)*64 + lane, i.e. key row slot / NCH and swizzled chunk slot % NCH.
-  int ld_row[TL::LOADS], ld_kch[TL::LOADS], ld_vch[TL::LOADS];
+  // Per-lane source byte offsets of the direct loads within a tile: load i of this wave
+  // fills LDS slots (wave*LOADS + i)*64 + lane, i.e. key row slot / NCH and swizzled
+  // chunk slot % NCH. The tile base is wave-uniform (scalar registers).
+  int ld_koff[TL::LOADS], ld_voff[TL::LOADS];
 #pragma unroll
   for (int i = 0; i < TL::LOADS; ++i) {
     const int slot = (wave * TL::LOADS + i) * 64 + lane;
     const int row = slot / TL::NCH, pch = slot % TL::NCH;
-    ld_row[i] = row;
-    ld_kch[i] = (pch ^ swz_k<D>(row)) * 8;
-    ld_vch[i] = (pch ^ swz_v<D>(row)) * 8;
+    ld_koff[i] = (int)(row * p.sks * 2) + (pch ^ swz_k<D>(row)) * 16;
+    ld_voff[i] = (int)(row * p.sks * 2) + (pch ^ swz_v<D>(row)) * 16;
   }
+  const char* kgb = reinterpret_cast<const char*>(kg);
+  const char* vgb = reinterpret_cast<const char*>(vg);
   auto issue = [&](int kt, int stage) {
     const int64_t key0 = (int64_t)kt * BN;
+    const char* kt_base = kgb + key0 * p.sks * 2;
+    const char* vt_base = vgb + key0 * p.sks * 2;
+    char* kdst = smem + (2 * stage) * TL::TILEB + wave * TL::LOADS * 1024;
+    char* vdst = smem + (2 * stage + 1) * TL::TILEB + wave * TL::LOADS * 1024;
+    if (key0 + BN <= S) {
 #pragma unroll
-    for (int i = 0; i < TL::LOADS; ++i) {
-      int64_t key = key0 + ld_row[i];
-      if (key > S - 1) key = S - 1;  // rows past the end are masked; read a valid one
-      const T* ksrc = kg + key * p.sks + ld_kch[i];
-      const T* vsrc = vg + key * p.sks + ld_vch[i];
-      __builtin_amdgcn_global_load_lds((const void*)ksrc,
-                                       (lds_void*)(smem[stage][0] + (wave * TL::LOADS + i) * 1024),
-                                       16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)vsrc,
-                                       (lds_void*)(smem[stage][1] + (wave * TL::LOADS + i) * 1024),
-                                       16, 0, 0);
+      for (int i = 0; i < TL::LOADS; ++i) {
+        __builtin_amdgcn_global_load_lds((const void*)(kt_base + (unsigned)ld_koff[i]),
+                                         (lds_void*)(kdst + i * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(vt_base + (unsigned)ld_voff[i]),
+                                         (lds_void*)(vdst + i * 1024), 16, 0, 0);
+      }
+    } else {
+      // last, partial tile: rows past the end are masked; they read row S - 1 instead
+#pragma unroll
+      for (int i = 0; i < TL::LOADS; ++i) {
+        const int slot = (wave * TL::LOADS + i) * 64 + lane;
+        const int row = slot / TL::NCH, pch = slot % TL::NCH;
+        const int64_t key = key0 + row < S ? key0 + row : S - 1;
+        const int64_t rb = (key - key0) * p.sks * 2;
+        __builtin_amdgcn_global_load_lds((const void*)(kt_base + rb + (pch ^ swz_k<D>(row)) * 16),
+                                         (lds_void*)(kdst + i * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(vt_base + rb + (pch ^ swz_v<D>(row)) * 16),
+                                         (lds_void*)(vdst + i * 1024), 16, 0, 0);
+      }
     }
   };
-  if (kt_begin <= kt_end) issue(kt_begin, 0);
+  issue(kt_begin, 0);
+#pragma unroll
+  for (int j = 1; j < TL::STAGES - 1; ++j)
+    if (kt_begin + j <= kt_end) issue(kt_begin + j, j);
 
   // ---- Q: load, fused RMSNorm + RoPE, one rounding, kept as MFMA B operands. Lane
   // (n, hi) holds channels 16s + 8hi + e; gains and RoPE rows come in 16-byte loads.
@@ -254,11 +287,15 @@ void prefill_kernel(PrefillParams p) {
       for (int e = 0; e < 8; ++e) qreg[s][e] = from_f32<T>(qf[s][e]);
   }
 
-  // this wave's query span (tile skipping and the mask-free fast path)
+  // this wave's query span (tile skipping and the mask-free fast path); positions fit
+  // in 32 bits (host check)
   const int w_first = qt * kBM + wave * 32;
   const int w_last = w_first + 31 < p.T - 1 ? w_first + 31 : p.T - 1;
   const bool wave_any = w_first < p.T;
-  const int64_t wq_lo = p.offset + w_first, wq_hi = p.offset + w_last;
+  const int off = (int)p.offset;
+  const int wq_lo = off + w_first, wq_hi = off + w_last;
+  const int S32 = (int)S;
+  const int qpos32 = (int)qpos;
 
   // LDS read offsets (bytes within a stage buffer).
   // K operand: row 32kb + n, chunk 2s + hi, swizzled by row & 15 == n & 15.
@@ -281,54 +318,81 @@ void prefill_kernel(PrefillParams p) {
   const float c = p.scale_log2;
 
   for (int kt = kt_begin; kt <= kt_end; ++kt) {
-    const int stage = (kt - kt_begin) & 1;
-    wait_vm_all();
-    __syncthreads();  // tile kt is in LDS for every wave; stage^1 is free again
-    if (kt + 1 <= kt_end) issue(kt + 1, stage ^ 1);
+    const int idx = kt - kt_begin;
+    const int stage = idx % TL::STAGES;
+    // Tile kt has landed once at most the loads of the tiles issued after it remain.
+    if (TL::STAGES == 3 && kt + 1 <= kt_end) wait_vm<2 * TL::LOADS>();
+    else wait_vm<0>();
+    __syncthreads();  // tile kt is in LDS for every wave; the stage of tile kt-1 is free
+    if (kt + TL::STAGES - 1 <= kt_end) issue(kt + TL::STAGES - 1, (idx + TL::STAGES - 1) % TL::STAGES);
 
-    const int64_t key0 = (int64_t)kt * BN;
+    const int key0 = kt * BN;
     const bool wave_needs = wave_any && key0 <= wq_hi &&
                             (p.window <= 0 || key0 + BN - 1 > wq_lo - p.window);
     if (!wave_needs) continue;
-    const bool full = key0 + BN - 1 <= wq_lo && key0 + BN - 1 < S &&
+    const bool full = key0 + BN - 1 <= wq_lo && key0 + BN - 1 < S32 &&
                       (p.window <= 0 || wq_hi - key0 < p.window) && w_last - w_first == 31;
 
-    const char* kl = smem[stage][0];
-    const char* vl = smem[stage][1];
+    const char* kl = smem + (2 * stage) * TL::TILEB + k_rd;
+    const char* vl = smem + (2 * stage + 1) * TL::TILEB;
 
-    // ---- S^T = K . Q^T
+    // ---- S^T = K . Q^T: KB independent accumulation chains, K operands read one
+    // k-step ahead of the MFMAs that use them.
     floatx16 sacc[KB];
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int x = 0; x < 16; ++x) sacc[kb][x] = 0.0f;
+    {
+      auto kread = [&](int kb, int st) {
+        return *reinterpret_cast<const V8*>(kl + kb * 32 * TL::ROWB + (((2 * st + hi) ^ k_sw) << 4));
+      };
+      V8 a[KB];
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        const V8 a = *reinterpret_cast<const V8*>(
-            kl + kb * 32 * TL::ROWB + k_rd + (((2 * s + hi) ^ k_sw) << 4));
-        sacc[kb] = Mfma<T>::run(a, qreg[s], sacc[kb]);
+      for (int kb = 0; kb < KB; ++kb) a[kb] = kread(kb, 0);
+#pragma unroll
+      for (int st = 0; st < KSTEPS; ++st) {
+        V8 an[KB];
+        if (st + 1 < KSTEPS) {
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) an[kb] = kread(kb, st + 1);
+        }
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) sacc[kb] = Mfma<T>::run(a[kb], qreg[st], sacc[kb]);
+        if (st + 1 < KSTEPS) {
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) a[kb] = an[kb];
+        }
       }
     }
 
-    // ---- online softmax (base 2, scale folded into the exponent)
-    float mx = kNegInf;
-    if (full) {
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int x = 0; x < 16; ++x) mx = fmaxf(mx, sacc[kb][x]);
-    } else {
+    // ---- mask (boundary tiles only): element (kb, x) of this lane is key
+    // key0 + 4hi + ce with ce = 32kb + 8(x/4) + x%4; it is visible iff lo <= ce <= hi.
+    if (!full) {
+      const int base = key0 + 4 * hi;
+      const int top = (qpos32 < S32 - 1 ? qpos32 : S32 - 1) - base;
+      const int lim_hi = valid_q ? top : -1;
+      const int lim_lo = p.window > 0 ? qpos32 - p.window + 1 - base : -(1 << 30);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int x = 0; x < 16; ++x) {
-          const int64_t key = key0 + kb * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);
-          const bool ok = valid_q && key <= qpos && key < S &&
-                          (p.window <= 0 || qpos - key < p.window);
-          if (!ok) sacc[kb][x] = kNegInf;
-          mx = fmaxf(mx, sacc[kb][x]);
+          const int ce = 32 * kb + 8 * (x >> 2) + (x & 3);
+          sacc[kb][x] = (ce <= lim_hi && ce >= lim_lo) ? sacc[kb][x] : kNegInf;
         }
     }
+
+    // ---- online softmax (base 2, scale folded into the exponent)
+    float mxp[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mxp[i] = sacc[0][4 * i];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int j = (kb == 0 ? 1 : 0); j < 4; ++j) mxp[i] = fmaxf(mxp[i], sacc[kb][4 * i + j]);
+    }
+    float mx = fmaxf(fmaxf(mxp[0], mxp[1]), fmaxf(mxp[2], mxp[3]));
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
     const float mxc = mx * c;
     if (mxc > m_run + kLazyLog2) {
@@ -340,17 +404,17 @@ void prefill_kernel(PrefillParams p) {
         for (int x = 0; x < 16; ++x) oacc[d][x] *= alpha;
       m_run = mxc;
     }
-    const float m_eff = m_run == kNegInf ? 0.0f : m_run;  // all -inf so far: weights 0
-    float rsum = 0.0f;
+    const float neg_m = m_run == kNegInf ? 0.0f : -m_run;  // all -inf so far: weights 0
+    float rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int x = 0; x < 16; ++x) {
-        const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kb][x], c, -m_eff));
+        const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kb][x], c, neg_m));
         sacc[kb][x] = pv;
-        rsum += pv;
+        rs[x & 3] += pv;
       }
-    l_run += rsum;
+    l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
 
     // ---- O^T += V^T . P^T
 #pragma unroll
@@ -389,16 +453,31 @@ void prefill_kernel(PrefillParams p) {
     }
 }
 
+template <typename T, int D>
+static int launch_prefill_d(PrefillParams p, hipStream_t s) {
+  using TL = Tile<D>;
+  static bool attr_set = false;  // raise the dynamic LDS limit once per kernel
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<T, D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, TL::LDS_BYTES) != hipSuccess)
+      return set_error("forge_attn_prefill: cannot reserve the LDS the kernel needs");
+    attr_set = true;
+  }
+  p.nqt = (p.T + TL::BM - 1) / TL::BM;
+  if ((int64_t)p.nqt * p.H * p.B > 0x7fffffff) return set_error("grid too large");
+  const dim3 grid((unsigned)((int64_t)p.nqt * p.H * p.B));
+  hipLaunchKernelGGL((prefill_kernel<T, D>), grid, dim3(TL::WAVES * 64), TL::LDS_BYTES, s, p);
+  return check_launch();
+}
+
 template <typename T>
 static int launch_prefill(const PrefillParams& p, int D, hipStream_t s) {
-  const dim3 grid((unsigned)((int64_t)p.nqt * p.H * p.B));
   switch (D) {
-    case 64: hipLaunchKernelGGL((prefill_kernel<T, 64>), grid, dim3(256), 0, s, p); break;
-    case 128: hipLaunchKernelGGL((prefill_kernel<T, 128>), grid, dim3(256), 0, s, p); break;
-    case 256: hipLaunchKernelGGL((prefill_kernel<T, 256>), grid, dim3(256), 0, s, p); break;
+    case 64: return launch_prefill_d<T, 64>(p, s);
+    case 128: return launch_prefill_d<T, 128>(p, s);
+    case 256: return launch_prefill_d<T, 256>(p, s);
     default: return set_error("forge_attn_prefill: head dim must be 64, 128 or 256");
   }
-  return check_launch();
 }
 
 }  // namespace forge
@@ -428,6 +507,8 @@ extern "C" int forge_attn_prefill(int dtype, int B, int T, int H, int K, int D, 
   if ((sqb | sqh | sqt | skb | skh | sks) % 8)
     return set_error("forge_attn_prefill: q/k/v strides must be multiples of 8 elements");
   if ((sob | sot | soh) % 4) return set_error("forge_attn_prefill: out strides must be multiples of 4");
+  if (offset + (int64_t)T + 256 >= (1LL << 31)) return set_error("forge_attn_prefill: positions must fit in 31 bits");
+  if (sks * 2 * 256 >= (1LL << 31)) return set_error("forge_attn_prefill: k/v row stride too large");
   if (((uintptr_t)q_weight | (uintptr_t)cos | (uintptr_t)sin) % 16 || (cos && s_cos_t % 4))
     return set_error("forge_attn_prefill: gain and RoPE rows must be 16-byte aligned");
   PrefillParams p{};
@@ -452,7 +533,6 @@ extern "C" int forge_attn_prefill(int dtype, int B, int T, int H, int K, int D, 
   p.H = H;
   p.K = K;
   p.G = H / K;
-  p.nqt = (T + kBM - 1) / kBM;
   p.xcd_map = (B * K) % 8 == 0 ? 1 : 0;
   p.window = window;
   p.scale_log2 = scale * kLog2e;
@@ -460,7 +540,6 @@ extern "C" int forge_attn_prefill(int dtype, int B, int T, int H, int K, int D, 
   p.sob = sob;
   p.sot = sot;
   p.soh = soh;
-  if ((int64_t)p.nqt * H * B > 0x7fffffff) return set_error("grid too large");
   hipStream_t s = (hipStream_t)stream;
   return dtype == FORGE_BF16 ? launch_prefill<bf16>(p, D, s) : launch_prefill<f16>(p, D, s);
 }
