@@ -26,13 +26,22 @@
 // equals the decode of that token alone, bit for bit (same chunk).
 #include <limits.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "forge_internal.h"
 
 namespace forge {
 
+#ifndef FORGE_SPLIT_NK
+#define FORGE_SPLIT_NK 2
+#endif
+#ifndef FORGE_SPLIT_PF
+#define FORGE_SPLIT_PF 3
+#endif
 constexpr int kSplitThreads = 256;
-constexpr int kSplitNK = 4;  // keys per group per iteration
+constexpr int kSplitNK = FORGE_SPLIT_NK;  // keys per group per iteration
+constexpr int kSplitPF = FORGE_SPLIT_PF;  // register buffers: loads run PF - 1 iterations ahead
 constexpr int kMaxChunk = 512;
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale: weights stay <= 2^8
 
@@ -60,6 +69,7 @@ struct SplitParams {
   int max_chunks;
   void* out;
   int64_t sob, sot, soh;
+  int persist;    // 1: persistent grid walking the unit list (splitk_kernel)
   float2* ws_ml;  // [B*H*T][max_chunks] (m, l)
   float* ws_o;    // [B*H*T][max_chunks][D]
 };
@@ -167,28 +177,32 @@ __device__ __forceinline__ uint4 load_q_row(const SplitParams& p, int b, int h, 
   return pack16<T>(q);
 }
 
+constexpr int kSplitWaves = kSplitThreads / kWave;
+
+// LDS of the block-level merge, reused by every unit a block processes.
+template <int D, int ROWS> struct SplitShared {
+  float o[kSplitWaves][ROWS][D];
+  float m[kSplitWaves][ROWS];
+  float l[kSplitWaves][ROWS];
+};
+
+// One work unit: rows rb*ROWS .. of KV head kvh of batch row b, keys of chunk c. The
+// caller guarantees the block is converged (the unit may leave early, block-uniformly).
 template <typename T, int D, int ROWS>
-__global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
+__device__ __forceinline__ void split_unit(const SplitParams& p, const int b, const int kvh,
+                                           const int rb, const int c, SplitShared<D, ROWS>& sh) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int LPR = D / VEC;  // lanes per key row
   static_assert(LPR >= 2 && LPR <= kWave && (LPR & (LPR - 1)) == 0, "bad head dim");
   constexpr int NG = kSplitThreads / LPR;  // key groups per block
   constexpr int NK = kSplitNK;
   constexpr int KPI = NG * NK;  // keys per block iteration
-  constexpr int NWAVES = kSplitThreads / kWave;
-
-  __shared__ float sh_o[NWAVES][ROWS][D];
-  __shared__ float sh_m[NWAVES][ROWS];
-  __shared__ float sh_l[NWAVES][ROWS];
+  constexpr int NWAVES = kSplitWaves;
 
   const int tid = threadIdx.x;
   const int li = tid % LPR;
   const int g = tid / LPR;
   const int wave = tid / kWave;
-  const int c = blockIdx.x;
-  const int kvh = blockIdx.y % p.K;
-  const int rb = blockIdx.y / p.K;
-  const int b = blockIdx.z;
 
   // Positions fit in 32 bits (host check: max_len < 2^31).
   const int base = (int)row_base(p.row_pos, p.pos_dev, p.pos0, b);
@@ -240,8 +254,11 @@ __global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
     }
   };
 
-  uint4 ka[NK], va[NK], kb[NK], vb[NK];
-  load_iter(it_first, ka, va);
+  constexpr int PF = kSplitPF;
+  uint4 kbuf[PF][NK], vbuf[PF][NK];
+#pragma unroll
+  for (int j = 0; j < PF - 1; ++j)
+    if (it_first + j <= it_last) load_iter(it_first + j, kbuf[j], vbuf[j]);
 
   uint4 q[ROWS];
 #pragma unroll
@@ -314,12 +331,16 @@ __global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
     }
   };
 
-  for (int it = it_first; it <= it_last; it += 2) {
-    if (it + 1 <= it_last) load_iter(it + 1, kb, vb);
-    compute_iter(it, ka, va);
-    if (it + 1 > it_last) break;
-    if (it + 2 <= it_last) load_iter(it + 2, ka, va);
-    compute_iter(it + 1, kb, vb);
+  // Rotating register pipeline: iteration it reads buffer (it - it_first) % PF and the
+  // loads of iteration it + PF - 1 are issued just before it is computed.
+  for (int it = it_first; it <= it_last; it += PF) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int cur = it + j;
+      if (cur > it_last) break;
+      if (cur + PF - 1 <= it_last) load_iter(cur + PF - 1, kbuf[(j + PF - 1) % PF], vbuf[(j + PF - 1) % PF]);
+      compute_iter(cur, kbuf[j], vbuf[j]);
+    }
   }
 
   // Merge the groups of this wave: butterfly over lane distances LPR .. 32.
@@ -345,10 +366,10 @@ __global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) sh_o[wave][r][li * VEC + e] = o[r][e];
+      for (int e = 0; e < VEC; ++e) sh.o[wave][r][li * VEC + e] = o[r][e];
       if (li == 0) {
-        sh_m[wave][r] = m[r];
-        sh_l[wave][r] = l[r];
+        sh.m[wave][r] = m[r];
+        sh.l[wave][r] = l[r];
       }
     }
   }
@@ -365,15 +386,15 @@ __global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
     int rkmin, rkmax;
     visible_range32(base + t, p.window, (int)p.max_len, rkmin, rkmax);
     if (c0 > rkmax || c0 + p.chunk - 1 < rkmin) continue;  // this chunk is outside the row
-    float M = sh_m[0][r];
+    float M = sh.m[0][r];
 #pragma unroll
-    for (int w = 1; w < NWAVES; ++w) M = fmaxf(M, sh_m[w][r]);
+    for (int w = 1; w < NWAVES; ++w) M = fmaxf(M, sh.m[w][r]);
     float L = 0.0f, O = 0.0f;
 #pragma unroll
     for (int w = 0; w < NWAVES; ++w) {
-      const float a = rescale(sh_m[w][r], M);
-      L = L + a * sh_l[w][r];
-      O = O + a * sh_o[w][r][e];
+      const float a = rescale(sh.m[w][r], M);
+      L = L + a * sh.l[w][r];
+      O = O + a * sh.o[w][r][e];
     }
     const int cmin = rkmin / p.chunk;
     const int cmax = rkmax / p.chunk;
@@ -386,6 +407,85 @@ __global__ __launch_bounds__(kSplitThreads) void splitk_kernel(SplitParams p) {
       p.ws_o[slot * D + e] = O;
       if (e == 0) p.ws_ml[slot] = make_float2(M, L);
     }
+  }
+}
+
+// Split-K kernel. Persistent mode (p.persist): a fixed grid of about as many blocks as
+// the GPU holds at once; every block derives the per-row chunk ranges from the device
+// positions (so the launch needs no host knowledge of ragged lengths and stays
+// graph-safe), builds the prefix sum of work units per batch row in LDS, and walks the
+// units u = blockIdx.x, blockIdx.x + gridDim.x, ... Units are ordered (row b, KV head x
+// row block, chunk) with the chunk fastest, so the units in flight stream neighbouring
+// chunks of a few (b, kv head) slabs, and no block is spent on chunks past a row's end.
+// Grid mode (batches too large for the LDS prefix): one block per (chunk, head x row
+// block, batch row), as before.
+constexpr int kPersistMaxRows = 2048;
+
+// Occupancy target: more waves hide more HBM latency, fewer leave registers for the
+// accumulators of ROWS query rows.
+template <int ROWS> constexpr int split_waves_per_eu() { return ROWS <= 2 ? 4 : ROWS == 4 ? 3 : 2; }
+
+template <typename T, int D, int ROWS>
+__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(split_waves_per_eu<ROWS>())))
+void splitk_kernel(SplitParams p) {
+  __shared__ SplitShared<D, ROWS> sh;
+  if (!p.persist) {
+    split_unit<T, D, ROWS>(p, blockIdx.z, blockIdx.y % p.K, blockIdx.y / p.K, blockIdx.x, sh);
+    return;
+  }
+  __shared__ int sh_pref[kPersistMaxRows + 1];
+  __shared__ int sh_cmin[kPersistMaxRows];
+  __shared__ int sh_nch[kPersistMaxRows];
+  const int tid = threadIdx.x;
+  const int n_rb = (p.rows_total + ROWS - 1) / ROWS;
+  const int per_row = p.K * n_rb;  // (kv head, row block) pairs per chunk
+  // chunk range of each batch row: union of its T queries' visible keys
+  for (int b = tid; b < p.B; b += kSplitThreads) {
+    const int base = (int)row_base(p.row_pos, p.pos_dev, p.pos0, b);
+    int lo, hi0, lo1, hi;
+    visible_range32(base, p.window, (int)p.max_len, lo, hi0);
+    visible_range32(base + p.T - 1, p.window, (int)p.max_len, lo1, hi);
+    const int cmin = lo / p.chunk;
+    int cmax = hi / p.chunk;
+    if (cmax > p.max_chunks - 1) cmax = p.max_chunks - 1;
+    sh_cmin[b] = cmin;
+    sh_nch[b] = (hi >= lo && cmax >= cmin) ? cmax - cmin + 1 : 0;
+  }
+  __syncthreads();
+  // exclusive prefix sum of units per row (wave 0: lane l scans a contiguous segment)
+  if (tid < kWave) {
+    const int seg = (p.B + kWave - 1) / kWave;
+    const int r0 = tid * seg;
+    const int r1 = r0 + seg < p.B ? r0 + seg : p.B;
+    int sum = 0;
+    for (int r = r0; r < r1; ++r) sum += sh_nch[r] * per_row;
+    int incl = sum;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int v = __shfl_up(incl, d, kWave);
+      if (tid >= d) incl += v;
+    }
+    int run = incl - sum;
+    for (int r = r0; r < r1; ++r) {
+      sh_pref[r] = run;
+      run += sh_nch[r] * per_row;
+    }
+    if (tid == kWave - 1) sh_pref[p.B] = incl;
+  }
+  __syncthreads();
+  const int total = sh_pref[p.B];
+  for (int u = blockIdx.x; u < total; u += gridDim.x) {
+    int lo = 0, hi = p.B - 1;  // last row with sh_pref[row] <= u
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (sh_pref[mid] <= u) lo = mid;
+      else hi = mid - 1;
+    }
+    const int o = u - sh_pref[lo];
+    const int n = sh_nch[lo];
+    const int pr = o / n;
+    split_unit<T, D, ROWS>(p, lo, pr % p.K, pr / p.K, sh_cmin[lo] + o % n, sh);
+    __syncthreads();  // the next unit reuses the merge LDS
   }
 }
 
@@ -493,14 +593,57 @@ static int auto_chunk(int dtype, int B, int T, int H, int K, int D, int64_t max_
   return chunk;
 }
 
+// Blocks of `kernel` the current device holds at once (CUs x occupancy), cached per
+// (device, kernel); host queries only, so the launch stays graph-capturable.
+static int resident_blocks(const void* kernel) {
+  struct Entry { int dev; const void* k; int n; };
+  static Entry cache[64];
+  static int used = 0;
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i)
+    if (cache[i].dev == dev && cache[i].k == kernel) return cache[i].n;
+  int ncu = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kSplitThreads, 0) != hipSuccess) return 0;
+  const int n = ncu * (per_cu > 0 ? per_cu : 1);
+  if (used < 64) cache[used++] = Entry{dev, kernel, n};
+  return n;
+}
+
 template <typename T, int D>
-static int launch_split_d(const SplitParams& p, int rows, dim3 grid, hipStream_t s) {
+static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
+  const int n_rb = (p.rows_total + rows - 1) / rows;
+  const void* kern = nullptr;
+  switch (rows) {
+    case 1: kern = reinterpret_cast<const void*>(&splitk_kernel<T, D, 1>); break;
+    case 2: kern = reinterpret_cast<const void*>(&splitk_kernel<T, D, 2>); break;
+    case 4: kern = reinterpret_cast<const void*>(&splitk_kernel<T, D, 4>); break;
+    case 8: kern = reinterpret_cast<const void*>(&splitk_kernel<T, D, 8>); break;
+    default: return set_error("internal: rows per block");
+  }
+  dim3 grid;
+  if (p.B <= kPersistMaxRows) {
+    const int64_t upper = (int64_t)p.B * p.K * n_rb * p.max_chunks;
+    int blocks = resident_blocks(kern);
+    if (blocks <= 0) return set_error("forge_attn_decode: cannot query the device");
+    if (upper < blocks) blocks = (int)upper;
+    if ((int64_t)p.B * p.K * n_rb * p.max_chunks >= (1LL << 31))
+      return set_error("forge_attn_decode: too many work units");
+    p.persist = 1;
+    grid = dim3((unsigned)blocks);
+  } else {
+    if ((int64_t)p.K * n_rb > 65535 || p.B > 65535) return set_error("grid too large");
+    p.persist = 0;
+    grid = dim3((unsigned)p.max_chunks, (unsigned)(p.K * n_rb), (unsigned)p.B);
+  }
   switch (rows) {
 #define FORGE_ROWS(R) \
   case R: hipLaunchKernelGGL((splitk_kernel<T, D, R>), grid, dim3(kSplitThreads), 0, s, p); break;
     FORGE_ROWS(1) FORGE_ROWS(2) FORGE_ROWS(4) FORGE_ROWS(8)
 #undef FORGE_ROWS
-    default: return set_error("internal: rows per block");
   }
   int st = check_launch();
   if (st || p.max_chunks < 2) return st;
@@ -511,12 +654,12 @@ static int launch_split_d(const SplitParams& p, int rows, dim3 grid, hipStream_t
 }
 
 template <typename T>
-static int launch_split(const SplitParams& p, int D, int rows, dim3 grid, hipStream_t s) {
+static int launch_split(const SplitParams& p, int D, int rows, hipStream_t s) {
   switch (D) {
-    case 32: return launch_split_d<T, 32>(p, rows, grid, s);
-    case 64: return launch_split_d<T, 64>(p, rows, grid, s);
-    case 128: return launch_split_d<T, 128>(p, rows, grid, s);
-    case 256: return launch_split_d<T, 256>(p, rows, grid, s);
+    case 32: return launch_split_d<T, 32>(p, rows, s);
+    case 64: return launch_split_d<T, 64>(p, rows, s);
+    case 128: return launch_split_d<T, 128>(p, rows, s);
+    case 256: return launch_split_d<T, 256>(p, rows, s);
     default: return set_error("forge_attn_decode: head dim must be 32, 64, 128 or 256");
   }
 }
@@ -619,13 +762,10 @@ extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, c
     p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + ml);
   }
   const int rows = rows_per_block(p.rows_total);
-  const int n_rb = (p.rows_total + rows - 1) / rows;
-  if ((int64_t)K * n_rb > 65535 || B > 65535) return set_error("grid too large");
-  const dim3 grid((unsigned)p.max_chunks, (unsigned)(K * n_rb), (unsigned)B);
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
-    case FORGE_F32: return launch_split<float>(p, D, rows, grid, s);
-    case FORGE_BF16: return launch_split<bf16>(p, D, rows, grid, s);
-    default: return launch_split<f16>(p, D, rows, grid, s);
+    case FORGE_F32: return launch_split<float>(p, D, rows, s);
+    case FORGE_BF16: return launch_split<bf16>(p, D, rows, s);
+    default: return launch_split<f16>(p, D, rows, s);
   }
 }
