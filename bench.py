@@ -66,6 +66,8 @@ class DecodeWorkload:
         self.cos = cos[idx].to(dev)
         self.sin = sin[idx].to(dev)
         self.row_pos = base.to(torch.int32).to(dev)
+        # rows of one length use the host position, as the module does with a plain KVCache
+        self.pos = int(base[0]) if len(set(lens)) == 1 else None
         self.scale = 1.0 / math.sqrt(D)
         self.out = torch.empty(B, T, H, D, device=dev, dtype=dtype)
         from sleuth_amd import ops
@@ -79,16 +81,20 @@ class DecodeWorkload:
         from sleuth_amd import ops
 
         i = self.layer if layer is None else layer
-        ops.kv_append(self.k, self.v, self.k_caches[i], self.v_caches[i], row_pos=self.row_pos,
-                      k_weight=self.wk, eps=1e-6, norm_k=True, cos=self.cos, sin=self.sin)
+        where = dict(pos=self.pos) if self.pos is not None else dict(row_pos=self.row_pos)
+        cos, sin = (self.cos[0], self.sin[0]) if self.pos is not None else (self.cos, self.sin)
+        ops.kv_append(self.k, self.v, self.k_caches[i], self.v_caches[i], **where,
+                      k_weight=self.wk, eps=1e-6, norm_k=True, cos=cos, sin=sin)
 
     def attend(self, layer=None):
         from sleuth_amd import ops
 
         i = self.layer if layer is None else layer
-        return ops.attn_decode(self.q, self.k_caches[i], self.v_caches[i], scale=self.scale,
-                               row_pos=self.row_pos, max_kv_len=self.max_len, window=self.window,
-                               q_weight=self.wq, eps=1e-6, norm_q=True, cos=self.cos, sin=self.sin,
+        where = dict(pos=self.pos) if self.pos is not None else dict(row_pos=self.row_pos)
+        cos, sin = (self.cos[0], self.sin[0]) if self.pos is not None else (self.cos, self.sin)
+        return ops.attn_decode(self.q, self.k_caches[i], self.v_caches[i], scale=self.scale, **where,
+                               max_kv_len=self.max_len, window=self.window,
+                               q_weight=self.wq, eps=1e-6, norm_q=True, cos=cos, sin=sin,
                                chunk=self.chunk, out=self.out, workspace=self.ws)
 
     def step(self):

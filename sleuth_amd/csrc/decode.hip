@@ -410,7 +410,8 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
   }
 }
 
-// Split-K kernel. Persistent mode (p.persist): a fixed grid of about as many blocks as
+// Split-K kernel. Persistent mode (p.persist, used when positions come from device
+// memory): a fixed grid of about as many blocks as
 // the GPU holds at once; every block derives the per-row chunk ranges from the device
 // positions (so the launch needs no host knowledge of ragged lengths and stays
 // graph-safe), builds the prefix sum of work units per batch row in LDS, and walks the
@@ -625,7 +626,12 @@ static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
     default: return set_error("internal: rows per block");
   }
   dim3 grid;
-  if (p.B <= kPersistMaxRows) {
+  // Persistent only where the lengths live on the device (ragged rows, graph steps): there
+  // it saves the blocks a dense grid would spend past each row's end. With one host-known
+  // position the dense grid has no such blocks, and the hardware's dynamic block dispatch
+  // balances uneven per-CU bandwidth better than a fixed assignment does.
+  const bool device_lengths = p.row_pos != nullptr || p.pos_dev != nullptr;
+  if (device_lengths && p.B <= kPersistMaxRows) {
     const int64_t upper = (int64_t)p.B * p.K * n_rb * p.max_chunks;
     int blocks = resident_blocks(kern);
     if (blocks <= 0) return set_error("forge_attn_decode: cannot query the device");
