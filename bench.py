@@ -275,7 +275,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--extra", action="store_true", help="also print lines for configs C2, C3-decode, C5")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--only", choices=["decode", "prefill", "copy"],
+    ap.add_argument("--only", choices=["decode", "prefill", "copy", "extra"],
                     help="time one workload (for rocprofv3 runs); copy = a 1 GiB torch copy, the "
                          "known-size kernel that calibrates the HBM byte counters")
     args = ap.parse_args()
@@ -374,6 +374,8 @@ def run_only(args, dev) -> int:
         pf = PrefillWorkload(4, 4096, 16, 8, 128, 1e6, torch.bfloat16, dev)
         t = time_loop(pf.step, args.steps, args.warmup)
         print(json.dumps({"workload": "C3 prefill step", "us": round(t * 1e6, 2)}), flush=True)
+    elif args.only == "extra":
+        print(json.dumps(extra_configs(dev, args)), flush=True)
     else:
         n = 1 << 30
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)

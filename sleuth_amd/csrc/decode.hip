@@ -70,9 +70,21 @@ struct SplitParams {
   void* out;
   int64_t sob, sot, soh;
   int persist;    // 1: persistent grid walking the unit list (splitk_kernel)
+  int vec_tables; // 1: cos/sin rows and q gains are 16-byte aligned (vector loads)
   float2* ws_ml;  // [B*H*T][max_chunks] (m, l)
   float* ws_o;    // [B*H*T][max_chunks][D]
 };
+
+// Eight fp32 values: two 16-byte loads when the caller's tables allow it (a block-uniform
+// flag), else scalar loads of the same values.
+__device__ __forceinline__ void load_f32x8_any(const float* ptr, float* out, bool vec) {
+  if (vec) {
+    load_f32x8(ptr, out);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = ptr[e];
+  }
+}
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -569,6 +581,327 @@ __global__ __launch_bounds__(256) void combine_kernel(SplitParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Verify / decode for wide head groups (G = H/K >= 4, bf16/fp16, head dim 128 or 256) on
+// MFMA. There the G*T query rows of one KV head make a small GEMM rather than a GEMV, and
+// the VALU split-K kernel above spends its time on per-score lane reductions. One block
+// (4 waves) takes one unit of the same split as above: (batch row, KV head, block of up
+// to 32 rows, chunk of keys at absolute positions), writing the same outputs/partials for
+// the same combine kernel. The path is chosen by (dtype, head dim, G) only, never by T, so
+// a verify row and the decode of that token run the same code.
+//
+//   * K and V tiles of 32 keys go from HBM into LDS with direct loads (two stages), the
+//     same swizzled layouts as the prefill kernel. Every wave computes the whole score tile
+//     S^T = K . Q^T (32 keys x 32 rows on v_mfma_f32_32x32x16) with Q^T in registers, and
+//     owns D/4 output channels of O^T = V^T . P^T, so the waves never merge: the running
+//     (m, l) they keep are identical.
+//   * Lane l owns row l % 32 (a query head and token); the row's visible key range comes
+//     from its position as in the split kernel, so masks, windows and ragged rows match.
+template <int D> struct VerifyTile {
+  static constexpr int WAVES = 4;
+  static constexpr int ROWS = 32;
+  static constexpr int BN = 32;                 // keys per tile
+  static constexpr int NCH = D / 8;
+  static constexpr int ROWB = 2 * D;
+  static constexpr int TILEB = BN * ROWB;
+  static constexpr int LOADS = TILEB / (WAVES * 1024);
+  static constexpr int LDS_BYTES = 2 * 2 * TILEB;   // two stages of K and V
+  static constexpr int DW = D / WAVES;          // output channels per wave
+  static_assert(LOADS * WAVES * 1024 == TILEB, "tile must split into whole wave loads");
+  static_assert(DW % 32 == 0, "a wave owns whole 32-channel MFMA blocks");
+};
+
+typedef __bf16 v_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 v_f16x8 __attribute__((ext_vector_type(8)));
+typedef float v_floatx16 __attribute__((ext_vector_type(16)));
+typedef short v_i16x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct VMfma;
+template <> struct VMfma<bf16> {
+  typedef v_bf16x8 vec;
+  static __device__ __forceinline__ v_floatx16 run(vec a, vec b, v_floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct VMfma<f16> {
+  typedef v_f16x8 vec;
+  static __device__ __forceinline__ v_floatx16 run(vec a, vec b, v_floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// XOR swizzles of the 16-byte chunk index by key row (conflict-free operand reads; the
+// same as the prefill kernel's for head dim >= 128).
+__device__ __forceinline__ int vswz_k(int row) { return row & 15; }
+__device__ __forceinline__ int vswz_v(int row) { return (row & 3) << 2; }
+
+typedef __attribute__((address_space(3))) char v_lds_char;
+__device__ __forceinline__ unsigned v_lds_offset(const void* ptr) {
+  return (unsigned)(uintptr_t)(const v_lds_char*)ptr;
+}
+// global_load_lds_dwordx4 from inline asm (the compiler does not make later LDS reads wait
+// for it); M0 carries the LDS address and is restored.
+__device__ __forceinline__ void v_lds_dma16(const void* gbase, unsigned voff, unsigned lds) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(gbase), "s"(lds)
+      : "memory");
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void verify_mfma_kernel(SplitParams p) {
+  using V8 = typename VMfma<T>::vec;
+  using TL = VerifyTile<D>;
+  constexpr int BN = TL::BN;
+  constexpr int KSTEPS = D / 16;
+  constexpr int DBW = TL::DW / 32;  // 32-channel blocks per wave
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lane = tid % kWave;
+  const int n = lane & 31;
+  const int hi = lane >> 5;
+  const int c = blockIdx.x;
+  const int kvh = blockIdx.y % p.K;
+  const int rb = blockIdx.y / p.K;
+  const int b = blockIdx.z;
+
+  // this lane's row and its visible keys; the unit's key span (union over valid rows)
+  const int base = (int)row_base(p.row_pos, p.pos_dev, p.pos0, b);
+  const int flat = rb * TL::ROWS + n;
+  const bool valid = flat < p.rows_total;
+  const int t = valid ? flat / p.G : 0;
+  const int h = kvh * p.G + (valid ? flat % p.G : 0);
+  int kmin = INT_MAX, kmax = -1;
+  if (valid) visible_range32(base + t, p.window, (int)p.max_len, kmin, kmax);
+  // union over the unit's rows: both ends of a visible range grow with the position, so it
+  // runs from the first row's start to the last row's end (tokens rb*32/G .. of the unit)
+  int umin, umax, dummy;
+  {
+    const int r_hi = rb * TL::ROWS + TL::ROWS - 1 < p.rows_total - 1 ? rb * TL::ROWS + TL::ROWS - 1 : p.rows_total - 1;
+    visible_range32(base + rb * TL::ROWS / p.G, p.window, (int)p.max_len, umin, dummy);
+    visible_range32(base + r_hi / p.G, p.window, (int)p.max_len, dummy, umax);
+  }
+  const int c0 = c * p.chunk;
+  if (c0 > umax || c0 + p.chunk - 1 < umin) return;  // block-uniform
+  int t_first = umin > c0 ? (umin - c0) / BN : 0;
+  int t_last = (umax - c0) / BN;
+  if (t_last > p.chunk / BN - 1) t_last = p.chunk / BN - 1;
+  const int ntiles = t_last - t_first + 1;
+
+  // direct loads of tile i (key0 = c0 + (t_first + i)*BN) into stage i & 1; rows past the
+  // unit's last key read row umax (masked)
+  const char* kgb = reinterpret_cast<const char*>(static_cast<const T*>(p.kc) + b * p.skb + kvh * p.skh);
+  const char* vgb = reinterpret_cast<const char*>(static_cast<const T*>(p.vc) + b * p.skb + kvh * p.skh);
+  const int rstride = (int)p.sks * 2;
+  auto issue = [&](int i) {
+    if (i >= ntiles) return;
+    const int key0 = c0 + (t_first + i) * BN;
+    const int rows_left = umax - key0 + 1;
+    const unsigned kdst = v_lds_offset(smem + (2 * (i & 1)) * TL::TILEB + wave * TL::LOADS * 1024);
+    const unsigned vdst = kdst + TL::TILEB;
+    const char* kt = kgb + (int64_t)key0 * rstride;
+    const char* vt = vgb + (int64_t)key0 * rstride;
+#pragma unroll
+    for (int j = 0; j < TL::LOADS; ++j) {
+      const int slot = (wave * TL::LOADS + j) * 64 + lane;
+      const int row = slot / TL::NCH, pch = slot % TL::NCH;
+      const int rr = row < rows_left ? row : rows_left - 1;
+      v_lds_dma16(kt, (unsigned)(rr * rstride + ((pch ^ vswz_k(row)) << 4)), kdst + j * 1024);
+      v_lds_dma16(vt, (unsigned)(rr * rstride + ((pch ^ vswz_v(row)) << 4)), vdst + j * 1024);
+    }
+  };
+
+  // Q^T operands of this lane's row: channels 16s + 8hi + e, fused RMSNorm + RoPE in fp32,
+  // one rounding (as the split kernel's q prologue; the RoPE partner of channel x is x+D/2).
+  // The q loads go out before the first tile's direct loads: loads retire in order, so the
+  // q math then waits for q only.
+  V8 qreg[KSTEPS];
+  {
+    const T* src = static_cast<const T*>(p.q) + b * p.sqb + h * p.sqh + t * p.sqt;
+    uint4 qraw[KSTEPS];
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) qraw[s] = valid ? load16(src + 16 * s + 8 * hi) : make_uint4(0, 0, 0, 0);
+    issue(0);
+    float rs = 1.0f;  // RMSNorm factor (1 without FORGE_NORM_QK)
+    if (p.flags & FORGE_NORM_QK) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        float f[8];
+        unpack16<T>(qraw[s], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+      }
+      ss += __shfl_xor(ss, 32, kWave);
+      rs = rsqrtf(ss / (float)D + p.eps);
+    }
+    const bool gains = (p.flags & FORGE_NORM_QK) && p.qw;
+    const bool rope = (p.flags & FORGE_ROPE) && valid;
+    const float* cr = p.cos + b * p.csb + t * p.cst;
+    const float* sr = p.sin + b * p.csb + t * p.cst;
+    // channels x..x+7 (step s) and their RoPE partners x + D/2 (step s + KSTEPS/2)
+#pragma unroll
+    for (int s = 0; s < KSTEPS / 2; ++s) {
+      const int x = 16 * s + 8 * hi;
+      float a[8], z[8];
+      unpack16<T>(qraw[s], a);
+      unpack16<T>(qraw[s + KSTEPS / 2], z);
+      if (gains) {
+        float wa[8], wz[8];
+        load_f32x8_any(p.qw + x, wa, p.vec_tables);
+        load_f32x8_any(p.qw + x + D / 2, wz, p.vec_tables);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          a[e] = a[e] * rs * wa[e];
+          z[e] = z[e] * rs * wz[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          a[e] *= rs;
+          z[e] *= rs;
+        }
+      }
+      if (rope) {
+        float c1[8], s1[8], c2[8], s2[8];
+        load_f32x8_any(cr + x, c1, p.vec_tables);
+        load_f32x8_any(sr + x, s1, p.vec_tables);
+        load_f32x8_any(cr + x + D / 2, c2, p.vec_tables);
+        load_f32x8_any(sr + x + D / 2, s2, p.vec_tables);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float a0 = a[e], z0 = z[e];
+          a[e] = a0 * c1[e] - z0 * s1[e];
+          z[e] = z0 * c2[e] + a0 * s2[e];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        qreg[s][e] = from_f32<T>(a[e]);
+        qreg[s + KSTEPS / 2][e] = from_f32<T>(z[e]);
+      }
+    }
+  }
+
+  // LDS read offsets within a tile (as the prefill kernel's)
+  const int k_rd = n * TL::ROWB;
+  const int k_sw = vswz_k(n);
+  const int g = lane >> 4, kq = (lane >> 2) & 3, qq = lane & 3;
+  const int v_row = 4 * (g >> 1) + kq;
+  const int v_sw = vswz_v(v_row);
+  const int v_chlo = 2 * (g & 1) + (qq >> 1);
+  const int v_byte = 8 * (qq & 1);
+
+  v_floatx16 oacc[DBW];
+#pragma unroll
+  for (int d = 0; d < DBW; ++d)
+#pragma unroll
+    for (int x = 0; x < 16; ++x) oacc[d][x] = 0.0f;
+  float m_run = kNegInf, l_run = 0.0f;
+  const float cl2 = p.scale_log2;
+
+  for (int i = 0; i < ntiles; ++i) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's share of tile i landed
+    __syncthreads();                                  // every share; tile i-1's stage free
+    issue(i + 1);
+    const int key0 = c0 + (t_first + i) * BN;
+    const char* kl = smem + (2 * (i & 1)) * TL::TILEB + k_rd;
+    const char* vl = smem + (2 * (i & 1) + 1) * TL::TILEB;
+
+    // S^T = K . Q^T for the 32 keys of the tile
+    v_floatx16 sacc;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) sacc[x] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+      sacc = VMfma<T>::run(*reinterpret_cast<const V8*>(kl + (((2 * s + hi) ^ k_sw) << 4)), qreg[s], sacc);
+
+    // element x of this lane is key key0 + 8(x/4) + 4hi + x%4 of row n
+    const int lo = kmin - key0 - 4 * hi, top = kmax - key0 - 4 * hi;
+    float mx = kNegInf;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int ce = 8 * (x >> 2) + (x & 3);
+      sacc[x] = (ce >= lo && ce <= top) ? sacc[x] * cl2 : kNegInf;
+      mx = fmaxf(mx, sacc[x]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    if (mx > m_run + kRescaleLog2) {  // (m = -inf: first visible key)
+      const float alpha = m_run == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(m_run - mx);
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DBW; ++d)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) oacc[d][x] *= alpha;
+      m_run = mx;
+    }
+    float rs = 0.0f;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const float pv = sacc[x] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(sacc[x] - m_run);
+      sacc[x] = pv;
+      rs += pv;
+    }
+    l_run += rs;
+
+    // O^T += V^T . P^T over this wave's channels (two 16-key MFMA steps)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      V8 pb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pb[e] = from_f32<T>(sacc[8 * hf + e]);
+      const char* vrow0 = vl + (16 * hf + v_row) * TL::ROWB + v_byte;
+#pragma unroll
+      for (int d = 0; d < DBW; ++d) {
+        const int ch = ((4 * (wave * DBW + d) + v_chlo) ^ v_sw) << 4;
+        const v_i16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v_i16x4*)(vrow0 + ch));
+        const v_i16x4 vup = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v_i16x4*)(vrow0 + 8 * TL::ROWB + ch));
+        typedef short i16x8 __attribute__((ext_vector_type(8)));
+        const i16x8 av = __builtin_shufflevector(vlo, vup, 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[d] = VMfma<T>::run(__builtin_bit_cast(V8, av), pb, oacc[d]);
+      }
+    }
+  }
+
+  // The row's total over the two lane halves; the chunk's result: final output when the
+  // row's visible keys lie in this chunk only, else an fp32 partial (m, l, o).
+  l_run += __shfl_xor(l_run, 32, kWave);
+  if (!valid || c0 > kmax || c0 + p.chunk - 1 < kmin) return;
+  const int cmin = kmin / p.chunk, cmax = kmax / p.chunk;
+  // lane holds channels wave*DW + 32d + 8i + 4hi + j of row n
+  if (cmin == cmax) {
+    const float inv_l = 1.0f / l_run;
+    T* dst = static_cast<T*>(p.out) + b * p.sob + t * p.sot + h * p.soh + wave * TL::DW;
+#pragma unroll
+    for (int d = 0; d < DBW; ++d)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dst[32 * d + 8 * ii + 4 * hi + j] = from_f32<T>(oacc[d][4 * ii + j] * inv_l);
+  } else {
+    const int64_t rowid = ((int64_t)b * p.H + h) * p.T + t;
+    const int64_t slot = rowid * p.max_chunks + c;
+    float* dst = p.ws_o + slot * D + wave * TL::DW;
+#pragma unroll
+    for (int d = 0; d < DBW; ++d)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+        *reinterpret_cast<float4*>(dst + 32 * d + 8 * ii + 4 * hi) =
+            make_float4(oacc[d][4 * ii], oacc[d][4 * ii + 1], oacc[d][4 * ii + 2], oacc[d][4 * ii + 3]);
+    if (wave == 0 && hi == 0) p.ws_ml[slot] = make_float2(m_run, l_run);
+  }
+}
+
 // ---------------------------------------------------------------- host side
 static int vec_of(int dtype) { return dtype == FORGE_F32 ? 4 : 8; }
 
@@ -583,8 +916,23 @@ static int keys_per_iter(int dtype, int D) { return (kSplitThreads / (D / vec_of
 
 static bool head_dim_ok(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
 
+// The MFMA path (verify_mfma_kernel) serves bf16/fp16 head dim 128/256 with G >= 4 query
+// heads per KV head, whatever T is (so verify and decode of one model share it).
+static bool use_verify_mfma(int dtype, int D, int G) {
+  return dtype != FORGE_F32 && (D == 128 || D == 256) && G >= 4;
+}
+constexpr int kVerifyRows = 32;
+
 static int auto_chunk(int dtype, int B, int T, int H, int K, int D, int64_t max_kv_len) {
   const int G = H / K;
+  if (use_verify_mfma(dtype, D, G)) {
+    // 32-key tiles; about two blocks per CU (rows of T = 1, as the module asks for it)
+    const int64_t pairs = (int64_t)B * K * ((G * T + kVerifyRows - 1) / kVerifyRows);
+    const int64_t len = max_kv_len > 0 ? max_kv_len : 1;
+    int chunk = 32;
+    while (chunk * 2 <= kMaxChunk && pairs * ((len + chunk * 2 - 1) / (chunk * 2)) >= 512) chunk *= 2;
+    return chunk;
+  }
   const int rows = rows_per_block(G * T);
   const int64_t n_rb = (G * T + rows - 1) / rows;
   const int64_t pairs = (int64_t)B * K * n_rb;
@@ -659,6 +1007,34 @@ static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
   return check_launch();
 }
 
+template <typename T, int D>
+static int launch_verify_d(SplitParams p, hipStream_t s) {
+  using TL = VerifyTile<D>;
+  static bool attr_set = false;  // raise the dynamic LDS limit once per kernel
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_mfma_kernel<T, D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, TL::LDS_BYTES) != hipSuccess)
+      return set_error("forge_attn_decode: cannot reserve the LDS the kernel needs");
+    attr_set = true;
+  }
+  const int n_rb = (p.rows_total + kVerifyRows - 1) / kVerifyRows;
+  if ((int64_t)p.K * n_rb > 65535 || p.B > 65535) return set_error("grid too large");
+  p.persist = 0;
+  const dim3 grid((unsigned)p.max_chunks, (unsigned)(p.K * n_rb), (unsigned)p.B);
+  hipLaunchKernelGGL((verify_mfma_kernel<T, D>), grid, dim3(256), TL::LDS_BYTES, s, p);
+  int st = check_launch();
+  if (st || p.max_chunks < 2) return st;
+  const int64_t nrows = (int64_t)p.B * p.H * p.T;
+  if (nrows > 0x7fffffff) return set_error("too many rows");
+  hipLaunchKernelGGL((combine_kernel<T, D>), dim3((unsigned)nrows), dim3(256), 0, s, p);
+  return check_launch();
+}
+
+template <typename T>
+static int launch_verify(const SplitParams& p, int D, hipStream_t s) {
+  return D == 128 ? launch_verify_d<T, 128>(p, s) : launch_verify_d<T, 256>(p, s);
+}
+
 template <typename T>
 static int launch_split(const SplitParams& p, int D, int rows, hipStream_t s) {
   switch (D) {
@@ -720,7 +1096,8 @@ extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, c
     return set_error("KV cache full: pos + T exceeds the cache length");
   if (!row_pos && !pos_dev && pos0 + T > max_kv_len) max_kv_len = pos0 + T;
   if (window < 0) return set_error("window must be >= 0");
-  const int kpi = keys_per_iter(dtype, D);
+  const bool mfma_path = use_verify_mfma(dtype, D, H / K);
+  const int kpi = mfma_path ? 32 : keys_per_iter(dtype, D);
   if (chunk <= 0) chunk = auto_chunk(dtype, B, T, H, K, D, max_kv_len);
   if (chunk % kpi) return set_error("chunk must be a multiple of the keys per block iteration");
 
@@ -759,6 +1136,8 @@ extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, c
   p.sob = sob;
   p.sot = sot;
   p.soh = soh;
+  p.vec_tables = ((uintptr_t)q_weight | (uintptr_t)cos | (uintptr_t)sin) % 16 == 0 &&
+                 (cos == nullptr || (s_cos_b % 4 == 0 && s_cos_t % 4 == 0));
   if (p.max_chunks > 1) {
     const size_t need = forge_attn_decode_workspace_bytes(dtype, B, T, H, K, D, max_kv_len, chunk);
     if (!workspace || workspace_bytes < need) return set_error("workspace too small");
@@ -769,6 +1148,7 @@ extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, c
   }
   const int rows = rows_per_block(p.rows_total);
   hipStream_t s = (hipStream_t)stream;
+  if (mfma_path) return dtype == FORGE_BF16 ? launch_verify<bf16>(p, D, s) : launch_verify<f16>(p, D, s);
   switch (dtype) {
     case FORGE_F32: return launch_split<float>(p, D, rows, s);
     case FORGE_BF16: return launch_split<bf16>(p, D, rows, s);
