@@ -179,6 +179,33 @@ def time_loop(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(stop) / 1e3 / steps
 
 
+def time_graph(fn, n: int, replays: int, warmup: int) -> float:
+    """Seconds per call of fn(0) .. fn(n - 1) captured once in a HIP graph and replayed:
+    the GPU time of a call without the host's launch cost (the reference decodes under
+    CUDA graphs, cuda_graph.py:96-108). fn must not allocate."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(max(warmup, 1)):
+            for i in range(n):
+                fn(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / 1e3 / (replays * n)
+
+
 def read_traffic(name: str):
     """HBM bytes per launch of a kernel, measured with rocprofv3 --pmc (FETCH_SIZE and
     WRITE_SIZE, scaled by a copy kernel of known size) and recorded in the text summary
@@ -406,9 +433,12 @@ def extra_configs(dev, args) -> dict:
         t = time_loop(wl.step, args.steps * 4, args.warmup)
         ta = time_loop(lambda: (wl.attend(), setattr(wl, "layer", (wl.layer + 1) % len(wl.k_caches))),
                        args.steps * 4, args.warmup)
+        tg = time_graph(lambda i: wl.attend(i), len(wl.k_caches), args.steps, args.warmup)
         out[name] = {"step_us": round(t * 1e6, 2), "step_GBs": round(wl.step_bytes() / t / 1e9, 1),
                      "attention_call_us": round(ta * 1e6, 2),
-                     "attention_GBs": round(wl.attend_bytes() / ta / 1e9, 1), "chunk": wl.chunk}
+                     "attention_GBs": round(wl.attend_bytes() / ta / 1e9, 1),
+                     "attention_graph_us": round(tg * 1e6, 2),
+                     "attention_graph_GBs": round(wl.attend_bytes() / tg / 1e9, 1), "chunk": wl.chunk}
         print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         del wl
         torch.cuda.empty_cache()

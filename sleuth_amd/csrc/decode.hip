@@ -926,19 +926,32 @@ constexpr int kVerifyRows = 32;
 static int auto_chunk(int dtype, int B, int T, int H, int K, int D, int64_t max_kv_len) {
   const int G = H / K;
   if (use_verify_mfma(dtype, D, G)) {
-    // 32-key tiles; about two blocks per CU (rows of T = 1, as the module asks for it)
+    // The smallest multiple of 32 keys that puts every unit into one round of the device's
+    // block slots (two per CU): with one more unit than slots, the last few full units run
+    // as a second round and double the kernel's time. (rows of T = 1, as the module asks.)
     const int64_t pairs = (int64_t)B * K * ((G * T + kVerifyRows - 1) / kVerifyRows);
     const int64_t len = max_kv_len > 0 ? max_kv_len : 1;
-    int chunk = 32;
-    while (chunk * 2 <= kMaxChunk && pairs * ((len + chunk * 2 - 1) / (chunk * 2)) >= 512) chunk *= 2;
-    return chunk;
+    int ncu = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+      ncu = 256;
+    const int64_t slots = 2 * (int64_t)ncu;
+    const int64_t per_pair = slots / pairs > 1 ? slots / pairs : 1;  // chunks per (b, kv head, rows)
+    int64_t chunk = (len + per_pair - 1) / per_pair;
+    chunk = (chunk + 31) / 32 * 32;
+    return (int)(chunk < 32 ? 32 : chunk);
   }
   const int rows = rows_per_block(G * T);
   const int64_t n_rb = (G * T + rows - 1) / rows;
   const int64_t pairs = (int64_t)B * K * n_rb;
-  int chunk = keys_per_iter(dtype, D);
+  // At least 4 block iterations per unit (a one-iteration unit spends most of its time in
+  // the q prologue and the merge), then larger while about 2048 units remain.
+  const int kpi = keys_per_iter(dtype, D);
+  int chunk = kpi;
   const int64_t len = max_kv_len > 0 ? max_kv_len : 1;
-  while (chunk * 2 <= kMaxChunk && pairs * ((len + chunk * 2 - 1) / (chunk * 2)) >= 2048) chunk *= 2;
+  while (chunk * 2 <= kMaxChunk &&
+         (chunk < 4 * kpi || pairs * ((len + chunk * 2 - 1) / (chunk * 2)) >= 2048))
+    chunk *= 2;
   return chunk;
 }
 
