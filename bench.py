@@ -72,7 +72,7 @@ class DecodeWorkload:
         self.out = torch.empty(B, T, H, D, device=dev, dtype=dtype)
         from sleuth_amd import ops
 
-        self.chunk = ops.decode_chunk(dtype, B, T, H, K, D, self.max_len)
+        self.chunk = ops.decode_chunk(dtype, B, T, H, K, D, self.max_len, window)
         nbytes = ops.decode_workspace_bytes(dtype, B, T, H, K, D, self.max_len, self.chunk)
         self.ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
         self.layer = 0

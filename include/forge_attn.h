@@ -92,9 +92,11 @@ int forge_kv_append(int dtype, int B, int T, int K, int D, const void* k, int64_
  * q is the RAW projection when flags has FORGE_NORM_QK / FORGE_ROPE (norm + RoPE are
  * fused into the q load, gain q_weight), else already normalised.
  * max_kv_len: host upper bound on kv_len_b (sizes the grid); chunk: keys per split
- * (0 = forge_attn_decode_chunk). Rows are computed independently and a key's
- * contribution does not depend on T, so a verify row equals the decode of that token
- * alone bit for bit when both use the same chunk.
+ * (0 = forge_attn_decode_chunk over the span a row can see: window + 16 when a window
+ * is shorter than max_kv_len, else max_kv_len). Rows are computed independently and a
+ * key's contribution does not depend on T, so a verify row equals the decode of that
+ * token alone bit for bit when both use the same chunk (pass the chunk explicitly, or
+ * the same max_kv_len, to guarantee that).
  * workspace: device memory of forge_attn_decode_workspace_bytes(...) bytes.
  */
 int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, const void* q,
@@ -106,7 +108,8 @@ int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, const void* 
                       float scale, int chunk, void* out, int64_t sob, int64_t sot, int64_t soh,
                       void* workspace, size_t workspace_bytes, void* stream);
 
-/* Keys per split that forge_attn_decode picks for chunk = 0 (pure host function). */
+/* Keys per split for a row span of max_kv_len keys (pure host function). T is accepted
+ * for the signature but does not enter, so decode and verify steps of one layer agree. */
 int forge_attn_decode_chunk(int dtype, int B, int T, int H, int K, int D, int64_t max_kv_len);
 
 /* Workspace bytes forge_attn_decode needs (pure host function). */

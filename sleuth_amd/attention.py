@@ -144,7 +144,7 @@ class Attention(nn.Module):
             pos_kw, max_kv, offset, chunk = dict(pos=0), T, 0, 0
         else:
             kc, vc = cache.k[self.layer_idx], cache.v[self.layer_idx]
-            chunk = ops.decode_chunk(q.dtype, B, 1, H, self.n_kv, hd, cache.max_len)
+            chunk = ops.decode_chunk(q.dtype, B, 1, H, self.n_kv, hd, cache.max_len, self.window)
             if getattr(cache, "static", False):
                 pos = cache.positions
                 pos_kw, max_kv, offset = dict(pos_dev=pos), min(cache.length, cache.max_len), None

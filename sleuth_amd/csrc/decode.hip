@@ -923,7 +923,16 @@ static bool use_verify_mfma(int dtype, int D, int G) {
 }
 constexpr int kVerifyRows = 32;
 
-static int auto_chunk(int dtype, int B, int T, int H, int K, int D, int64_t max_kv_len) {
+// Default chunk. It does not depend on T, so decode and verify calls of one model get the
+// same chunk boundaries (and a verify row equals the decode of that token bit for bit);
+// with a sliding window, pass the span a row can see (window + kMaxVerifyT).
+constexpr int kMaxVerifyT = 16;
+static int64_t chunk_span(int64_t max_kv_len, int window) {
+  return window > 0 && window + kMaxVerifyT < max_kv_len ? window + kMaxVerifyT : max_kv_len;
+}
+
+static int auto_chunk(int dtype, int B, int /*T*/, int H, int K, int D, int64_t max_kv_len) {
+  const int T = 1;
   const int G = H / K;
   if (use_verify_mfma(dtype, D, G)) {
     // The smallest multiple of 32 keys that puts every unit into one round of the device's
@@ -1111,7 +1120,7 @@ extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, c
   if (window < 0) return set_error("window must be >= 0");
   const bool mfma_path = use_verify_mfma(dtype, D, H / K);
   const int kpi = mfma_path ? 32 : keys_per_iter(dtype, D);
-  if (chunk <= 0) chunk = auto_chunk(dtype, B, T, H, K, D, max_kv_len);
+  if (chunk <= 0) chunk = auto_chunk(dtype, B, T, H, K, D, chunk_span(max_kv_len, window));
   if (chunk % kpi) return set_error("chunk must be a multiple of the keys per block iteration");
 
   SplitParams p{};

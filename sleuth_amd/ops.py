@@ -153,8 +153,18 @@ def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: 
     check(st, "forge_kv_append")
 
 
-def decode_chunk(dtype: torch.dtype, B: int, T: int, H: int, K: int, D: int, max_kv_len: int) -> int:
-    return lib().forge_attn_decode_chunk(_DTYPES[dtype], B, T, H, K, D, int(max_kv_len))
+DECODE_CHUNK_MAX_T = 16  # the longest verify step the chunk span allows for (as the C default)
+
+
+def decode_chunk(dtype: torch.dtype, B: int, T: int, H: int, K: int, D: int, max_kv_len: int,
+                 window: int = 0) -> int:
+    """Default split-K chunk. T does not enter (decode and verify of a model share chunk
+    boundaries, so verify rows equal single-token decodes bit for bit); with a sliding window
+    it is sized for the keys a row can see, window + 16, not the cache length."""
+    span = int(max_kv_len)
+    if window > 0 and window + DECODE_CHUNK_MAX_T < span:
+        span = window + DECODE_CHUNK_MAX_T
+    return lib().forge_attn_decode_chunk(_DTYPES[dtype], B, T, H, K, D, span)
 
 
 def decode_workspace_bytes(dtype: torch.dtype, B: int, T: int, H: int, K: int, D: int,
@@ -194,8 +204,8 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *
     elif out.shape != (B, T, H, D) or out.dtype != q.dtype:
         raise ValueError(f"out must be [B,T,H,D] = {(B, T, H, D)} {q.dtype}")
     dt = dtype_code(q)
-    if chunk <= 0:
-        chunk = lib().forge_attn_decode_chunk(dt, B, T, H, K, D, max_kv_len)
+    if chunk <= 0:  # from the cache's capacity, not this call's length: stable across steps
+        chunk = decode_chunk(q.dtype, B, T, H, K, D, max_len, window)
     need = lib().forge_attn_decode_workspace_bytes(dt, B, T, H, K, D, max_kv_len, chunk)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
