@@ -114,6 +114,37 @@ __device__ __forceinline__ float rescale(float m_old, float m_new) {
   return m_old == kNegInf ? 0.0f : exp2f(m_old - m_new);
 }
 
+// ---------------------------------------------------------------- LDS direct loads
+typedef __attribute__((address_space(3))) char lds_char;
+__device__ __forceinline__ unsigned lds_offset(const void* ptr) {
+  return (unsigned)(uintptr_t)(const lds_char*)ptr;
+}
+// global_load_lds_dwordx4 (lane i's 16 bytes from gbase + voff land at LDS address
+// lds + 16 i) from inline asm: the compiler then does not make later LDS reads wait for
+// it, so the kernel waits for these loads itself (s_waitcnt vmcnt). M0 carries the LDS
+// address and is restored.
+__device__ __forceinline__ void lds_dma16(const void* gbase, unsigned voff, unsigned lds) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(gbase), "s"(lds)
+      : "memory");
+}
+
+// max over lanes l and l ^ 32 with gfx950's v_permlane32_swap (VALU, no LDS round trip):
+// swapping x with itself returns the lower half's and the upper half's value of the pair.
+// (The pair is read by value: __builtin_bit_cast of a vector element reads element 0.)
+__device__ __forceinline__ float max_xor32(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto c = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const unsigned c0 = c[0], c1 = c[1];
+  return fmaxf(__uint_as_float(c0), __uint_as_float(c1));
+}
+
 // Base position of batch row b (see include/forge_attn.h).
 __device__ __forceinline__ int64_t row_base(const int32_t* row_pos, const int64_t* pos_dev,
                                             int64_t pos0, int b) {

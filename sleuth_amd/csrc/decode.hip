@@ -635,24 +635,6 @@ template <> struct VMfma<f16> {
 __device__ __forceinline__ int vswz_k(int row) { return row & 15; }
 __device__ __forceinline__ int vswz_v(int row) { return (row & 3) << 2; }
 
-typedef __attribute__((address_space(3))) char v_lds_char;
-__device__ __forceinline__ unsigned v_lds_offset(const void* ptr) {
-  return (unsigned)(uintptr_t)(const v_lds_char*)ptr;
-}
-// global_load_lds_dwordx4 from inline asm (the compiler does not make later LDS reads wait
-// for it); M0 carries the LDS address and is restored.
-__device__ __forceinline__ void v_lds_dma16(const void* gbase, unsigned voff, unsigned lds) {
-  unsigned saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
-      "global_load_lds_dwordx4 %1, %2\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(voff), "s"(gbase), "s"(lds)
-      : "memory");
-}
-
 template <typename T, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void verify_mfma_kernel(SplitParams p) {
@@ -705,7 +687,7 @@ void verify_mfma_kernel(SplitParams p) {
     if (i >= ntiles) return;
     const int key0 = c0 + (t_first + i) * BN;
     const int rows_left = umax - key0 + 1;
-    const unsigned kdst = v_lds_offset(smem + (2 * (i & 1)) * TL::TILEB + wave * TL::LOADS * 1024);
+    const unsigned kdst = lds_offset(smem + (2 * (i & 1)) * TL::TILEB + wave * TL::LOADS * 1024);
     const unsigned vdst = kdst + TL::TILEB;
     const char* kt = kgb + (int64_t)key0 * rstride;
     const char* vt = vgb + (int64_t)key0 * rstride;
@@ -714,8 +696,8 @@ void verify_mfma_kernel(SplitParams p) {
       const int slot = (wave * TL::LOADS + j) * 64 + lane;
       const int row = slot / TL::NCH, pch = slot % TL::NCH;
       const int rr = row < rows_left ? row : rows_left - 1;
-      v_lds_dma16(kt, (unsigned)(rr * rstride + ((pch ^ vswz_k(row)) << 4)), kdst + j * 1024);
-      v_lds_dma16(vt, (unsigned)(rr * rstride + ((pch ^ vswz_v(row)) << 4)), vdst + j * 1024);
+      lds_dma16(kt, (unsigned)(rr * rstride + ((pch ^ vswz_k(row)) << 4)), kdst + j * 1024);
+      lds_dma16(vt, (unsigned)(rr * rstride + ((pch ^ vswz_v(row)) << 4)), vdst + j * 1024);
     }
   };
 
@@ -833,7 +815,7 @@ void verify_mfma_kernel(SplitParams p) {
       sacc[x] = (ce >= lo && ce <= top) ? sacc[x] * cl2 : kNegInf;
       mx = fmaxf(mx, sacc[x]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    mx = max_xor32(mx);
     if (mx > m_run + kRescaleLog2) {  // (m = -inf: first visible key)
       const float alpha = m_run == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(m_run - mx);
       l_run *= alpha;

@@ -39,7 +39,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) void lds_void;
 
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16> {
@@ -191,19 +190,20 @@ void prefill_kernel(PrefillParams p) {
   }
   const char* kgb = reinterpret_cast<const char*>(kg);
   const char* vgb = reinterpret_cast<const char*>(vg);
+  // The loads are issued from inline asm (lds_dma16), so the compiler does not hold the
+  // LDS reads of the current stage back until the next stage's loads have landed; the
+  // loop waits for them itself (wait_vm before the barrier).
   auto issue = [&](int kt, int stage) {
     const int64_t key0 = (int64_t)kt * BN;
     const char* kt_base = kgb + key0 * p.sks * 2;
     const char* vt_base = vgb + key0 * p.sks * 2;
-    char* kdst = smem + (2 * stage) * TL::TILEB + wave * TL::LOADS * 1024;
-    char* vdst = smem + (2 * stage + 1) * TL::TILEB + wave * TL::LOADS * 1024;
+    const unsigned kdst = lds_offset(smem + (2 * stage) * TL::TILEB + wave * TL::LOADS * 1024);
+    const unsigned vdst = kdst + TL::TILEB;
     if (key0 + BN <= S) {
 #pragma unroll
       for (int i = 0; i < TL::LOADS; ++i) {
-        __builtin_amdgcn_global_load_lds((const void*)(kt_base + (unsigned)ld_koff[i]),
-                                         (lds_void*)(kdst + i * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(vt_base + (unsigned)ld_voff[i]),
-                                         (lds_void*)(vdst + i * 1024), 16, 0, 0);
+        lds_dma16(kt_base, (unsigned)ld_koff[i], kdst + i * 1024);
+        lds_dma16(vt_base, (unsigned)ld_voff[i], vdst + i * 1024);
       }
     } else {
       // last, partial tile: rows past the end are masked; they read row S - 1 instead
@@ -212,11 +212,9 @@ void prefill_kernel(PrefillParams p) {
         const int slot = (wave * TL::LOADS + i) * 64 + lane;
         const int row = slot / TL::NCH, pch = slot % TL::NCH;
         const int64_t key = key0 + row < S ? key0 + row : S - 1;
-        const int64_t rb = (key - key0) * p.sks * 2;
-        __builtin_amdgcn_global_load_lds((const void*)(kt_base + rb + (pch ^ swz_k<D>(row)) * 16),
-                                         (lds_void*)(kdst + i * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(vt_base + rb + (pch ^ swz_v<D>(row)) * 16),
-                                         (lds_void*)(vdst + i * 1024), 16, 0, 0);
+        const unsigned rb = (unsigned)((key - key0) * p.sks * 2);
+        lds_dma16(kt_base, rb + (pch ^ swz_k<D>(row)) * 16, kdst + i * 1024);
+        lds_dma16(vt_base, rb + (pch ^ swz_v<D>(row)) * 16, vdst + i * 1024);
       }
     }
   };
@@ -336,8 +334,10 @@ void prefill_kernel(PrefillParams p) {
     const char* kl = smem + (2 * stage) * TL::TILEB + k_rd;
     const char* vl = smem + (2 * stage + 1) * TL::TILEB;
 
-    // ---- S^T = K . Q^T: KB independent accumulation chains, K operands read one
-    // k-step ahead of the MFMAs that use them.
+    // ---- S^T = K . Q^T: KB independent accumulation chains. The K operands of step
+    // st + 2 are read before the MFMAs of step st are issued (three register sets), so
+    // the LDS latency hides under two steps of MFMAs; the scheduling groups pin that
+    // order (left alone, the compiler reuses one register set and waits for every read).
     floatx16 sacc[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
@@ -347,21 +347,26 @@ void prefill_kernel(PrefillParams p) {
       auto kread = [&](int kb, int st) {
         return *reinterpret_cast<const V8*>(kl + kb * 32 * TL::ROWB + (((2 * st + hi) ^ k_sw) << 4));
       };
-      V8 a[KB];
+      V8 a0[KB], a1[KB], a2[KB];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) a[kb] = kread(kb, 0);
+      for (int kb = 0; kb < KB; ++kb) a0[kb] = kread(kb, 0);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) a1[kb] = kread(kb, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * KB, 0);
 #pragma unroll
       for (int st = 0; st < KSTEPS; ++st) {
-        V8 an[KB];
-        if (st + 1 < KSTEPS) {
+        if (st + 2 < KSTEPS) {
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) an[kb] = kread(kb, st + 1);
+          for (int kb = 0; kb < KB; ++kb) a2[kb] = kread(kb, st + 2);
+          __builtin_amdgcn_sched_group_barrier(0x100, KB, 0);
         }
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) sacc[kb] = Mfma<T>::run(a[kb], qreg[st], sacc[kb]);
-        if (st + 1 < KSTEPS) {
+        for (int kb = 0; kb < KB; ++kb) sacc[kb] = Mfma<T>::run(a0[kb], qreg[st], sacc[kb]);
+        __builtin_amdgcn_sched_group_barrier(0x008, KB, 0);
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) a[kb] = an[kb];
+        for (int kb = 0; kb < KB; ++kb) {
+          a0[kb] = a1[kb];
+          a1[kb] = a2[kb];
         }
       }
     }
@@ -393,7 +398,7 @@ void prefill_kernel(PrefillParams p) {
         for (int j = (kb == 0 ? 1 : 0); j < 4; ++j) mxp[i] = fmaxf(mxp[i], sacc[kb][4 * i + j]);
     }
     float mx = fmaxf(fmaxf(mxp[0], mxp[1]), fmaxf(mxp[2], mxp[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    mx = max_xor32(mx);
     const float mxc = mx * c;
     if (mxc > m_run + kLazyLog2) {
       const float alpha = m_run == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(m_run - mxc);

@@ -141,7 +141,7 @@ def test_decode_single_token(dtype, D, HK):
     assert max_abs(got, ref) <= tol(dtype)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("T", [2, 4, 5, 16])
 @pytest.mark.parametrize("window", [0, 64])
 def test_verify_multi_token(dtype, T, window):
@@ -164,11 +164,13 @@ def test_decode_prenormalised_q():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_verify_rows_equal_single_decodes_bitwise(dtype):
+@pytest.mark.parametrize("H,K,D", [(8, 2, 128), (8, 1, 256), (6, 2, 64)])
+def test_verify_rows_equal_single_decodes_bitwise(dtype, H, K, D):
     """A verify row (T = 5) equals decoding that token alone, bit for bit (same chunk):
-    the property speculative decoding relies on (fused_ops.py:19-20)."""
+    the property speculative decoding relies on (fused_ops.py:19-20). Covers the wide-group
+    MFMA kernel (G = 4, 8 at hd 128/256) and the VALU kernel (G = 3, fp32)."""
     g = gen(5)
-    B, H, K, D, T, L = 2, 8, 2, 128, 5, 1500
+    B, T, L = 2, 5, 1500
     kc = randn(g, B, K, L + 8, D, dtype=dtype).to(DEV)
     vc = randn(g, B, K, L + 8, D, dtype=dtype).to(DEV)
     q = randn(g, B, H, T, D, dtype=dtype).to(DEV)
@@ -180,9 +182,12 @@ def test_verify_rows_equal_single_decodes_bitwise(dtype):
             assert torch.equal(allv[:, t:t + 1], one), (window, t)
 
 
-def test_decode_pos_dev_matches_host_pos():
+@pytest.mark.parametrize("H,K", [(16, 8), (8, 1)])
+def test_decode_pos_dev_matches_host_pos(H, K):
+    """Device-held position (persistent grid) equals the host position (dense grid) bit for
+    bit, on the VALU kernel (G = 2) and the wide-group MFMA kernel (G = 8)."""
     g = gen(9)
-    B, H, K, D, T, L = 2, 16, 8, 128, 3, 900
+    B, D, T, L = 2, 128, 3, 900
     kc = randn(g, B, K, 1024, D, dtype=torch.bfloat16).to(DEV)
     vc = randn(g, B, K, 1024, D, dtype=torch.bfloat16).to(DEV)
     q = randn(g, B, H, T, D, dtype=torch.bfloat16).to(DEV)
