@@ -302,6 +302,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--extra", action="store_true", help="also print lines for configs C2, C3-decode, C5")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--config", default="", help="with --only extra: run only the configs whose name contains this")
     ap.add_argument("--only", choices=["decode", "prefill", "copy", "extra"],
                     help="time one workload (for rocprofv3 runs); copy = a 1 GiB torch copy, the "
                          "known-size kernel that calibrates the HBM byte counters")
@@ -425,6 +426,8 @@ def extra_configs(dev, args) -> dict:
         "C5_verify_b8_T4_8q1kv_hd256_window1024": dict(lens=[8196] * 8, H=8, K=1, D=256, theta=1e6, T=4,
                                                        window=1024, n_layers=12),
     }.items():
+        if args.config and args.config not in name:
+            continue
         lens = kw.pop("lens")
         wl = DecodeWorkload(lens, dtype=dt, dev=dev, **kw)
         for i in range(len(wl.k_caches)):
