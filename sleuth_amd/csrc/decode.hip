@@ -605,7 +605,10 @@ template <int D> struct VerifyTile {
   static constexpr int ROWB = 2 * D;
   static constexpr int TILEB = BN * ROWB;
   static constexpr int LOADS = TILEB / (WAVES * 1024);
-  static constexpr int LDS_BYTES = 2 * 2 * TILEB;   // two stages of K and V
+  static constexpr int STAGES = 4;              // LDS stages of K and V: three tiles in flight
+  static constexpr int MAX_TOK = ROWS / 4 + 1;  // tokens under one unit's rows (G >= 4)
+  static constexpr int TAB_BYTES = (1 + 2 * MAX_TOK) * D * 4;  // q gains, cos and sin rows
+  static constexpr int LDS_BYTES = STAGES * 2 * TILEB + TAB_BYTES;
   static constexpr int DW = D / WAVES;          // output channels per wave
   static_assert(LOADS * WAVES * 1024 == TILEB, "tile must split into whole wave loads");
   static_assert(DW % 32 == 0, "a wave owns whole 32-channel MFMA blocks");
@@ -634,6 +637,16 @@ template <> struct VMfma<f16> {
 // same as the prefill kernel's for head dim >= 128).
 __device__ __forceinline__ int vswz_k(int row) { return row & 15; }
 __device__ __forceinline__ int vswz_v(int row) { return (row & 3) << 2; }
+
+// Wait until at most N vector-memory loads of this wave are outstanding (they retire in
+// issue order, so everything issued before the last N has landed).
+template <int N> __device__ __forceinline__ void vwait_vm() {
+  static_assert(N == 0 || N == 4 || N == 8 || N == 16, "add the count");
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+}
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
@@ -678,8 +691,8 @@ void verify_mfma_kernel(SplitParams p) {
   if (t_last > p.chunk / BN - 1) t_last = p.chunk / BN - 1;
   const int ntiles = t_last - t_first + 1;
 
-  // direct loads of tile i (key0 = c0 + (t_first + i)*BN) into stage i & 1; rows past the
-  // unit's last key read row umax (masked)
+  // direct loads of tile i (key0 = c0 + (t_first + i)*BN) into stage i % STAGES; rows past
+  // the unit's last key read row umax (masked)
   const char* kgb = reinterpret_cast<const char*>(static_cast<const T*>(p.kc) + b * p.skb + kvh * p.skh);
   const char* vgb = reinterpret_cast<const char*>(static_cast<const T*>(p.vc) + b * p.skb + kvh * p.skh);
   const int rstride = (int)p.sks * 2;
@@ -687,7 +700,7 @@ void verify_mfma_kernel(SplitParams p) {
     if (i >= ntiles) return;
     const int key0 = c0 + (t_first + i) * BN;
     const int rows_left = umax - key0 + 1;
-    const unsigned kdst = lds_offset(smem + (2 * (i & 1)) * TL::TILEB + wave * TL::LOADS * 1024);
+    const unsigned kdst = lds_offset(smem + (2 * (i % TL::STAGES)) * TL::TILEB + wave * TL::LOADS * 1024);
     const unsigned vdst = kdst + TL::TILEB;
     const char* kt = kgb + (int64_t)key0 * rstride;
     const char* vt = vgb + (int64_t)key0 * rstride;
@@ -701,17 +714,62 @@ void verify_mfma_kernel(SplitParams p) {
     }
   };
 
-  // Q^T operands of this lane's row: channels 16s + 8hi + e, fused RMSNorm + RoPE in fp32,
-  // one rounding (as the split kernel's q prologue; the RoPE partner of channel x is x+D/2).
-  // The q loads go out before the first tile's direct loads: loads retire in order, so the
-  // q math then waits for q only.
-  V8 qreg[KSTEPS];
+  // ---- prologue: the first STAGES - 1 tiles' loads, this lane's q row, and the block's
+  // q gains and RoPE rows staged in LDS (one memory round trip for all of them; loaded per
+  // lane they took one round trip per 16 channels)
+  const bool gains = (p.flags & FORGE_NORM_QK) && p.qw;
+  const bool rope = (p.flags & FORGE_ROPE) != 0;
+  const int tok_lo = rb * TL::ROWS / p.G;
+  const int tok_hi = (rb * TL::ROWS + TL::ROWS - 1 < p.rows_total - 1 ? rb * TL::ROWS + TL::ROWS - 1 : p.rows_total - 1) / p.G;
+  const int ntok = tok_hi - tok_lo + 1;  // <= MAX_TOK for G >= 4
+  float* tab = reinterpret_cast<float*>(smem + TL::STAGES * 2 * TL::TILEB);  // [gains | cos tok | sin tok][D]
+#pragma unroll
+  for (int i = 0; i < TL::STAGES - 1; ++i) issue(i);
+  // q of this lane's row, loaded unconditionally (rows past the end read row 0 of head
+  // kvh * G and are zeroed below): a conditional load made the compiler wait for it here
+  uint4 qraw[KSTEPS];
   {
     const T* src = static_cast<const T*>(p.q) + b * p.sqb + h * p.sqh + t * p.sqt;
-    uint4 qraw[KSTEPS];
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) qraw[s] = valid ? load16(src + 16 * s + 8 * hi) : make_uint4(0, 0, 0, 0);
-    issue(0);
+    for (int s = 0; s < KSTEPS; ++s) qraw[s] = load16(src + 16 * s + 8 * hi);
+  }
+  {
+    // every value's load goes out before the first store (one round trip, not one per value)
+    constexpr int NV = ((1 + 2 * TL::MAX_TOK) * D + TL::WAVES * kWave - 1) / (TL::WAVES * kWave);
+    const int nrow = (gains ? 1 : 0) + (rope ? 2 * ntok : 0);
+    float v[NV];
+    int dsti[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int idx = tid + j * TL::WAVES * kWave;
+      dsti[j] = -1;
+      v[j] = 0.0f;
+      if (idx < nrow * D) {
+        const int r = idx / D, x = idx % D;
+        const int rr = gains ? r : r + 1;  // table row: 0 gains, 1..ntok cos, ntok+1.. sin
+        if (rr == 0) {
+          v[j] = p.qw[x];
+        } else {
+          const int tk = tok_lo + (rr - 1) % ntok;
+          v[j] = (rr <= ntok ? p.cos : p.sin)[b * p.csb + (int64_t)tk * p.cst + x];
+        }
+        dsti[j] = (rr == 0 ? 0 : (rr <= ntok ? rr : rr - ntok + TL::MAX_TOK)) * D + x;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+      if (dsti[j] >= 0) tab[dsti[j]] = v[j];
+  }
+  __syncthreads();  // tables in LDS (the tile loads may still be in flight)
+
+  // Q^T operands of this lane's row: channels 16s + 8hi + e, fused RMSNorm + RoPE in fp32,
+  // one rounding (as the split kernel's q prologue; the RoPE partner of channel x is x+D/2).
+  V8 qreg[KSTEPS];
+  {
+    if (!valid) {
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) qraw[s] = make_uint4(0, 0, 0, 0);
+    }
     float rs = 1.0f;  // RMSNorm factor (1 without FORGE_NORM_QK)
     if (p.flags & FORGE_NORM_QK) {
       float ss = 0.0f;
@@ -725,10 +783,8 @@ void verify_mfma_kernel(SplitParams p) {
       ss += __shfl_xor(ss, 32, kWave);
       rs = rsqrtf(ss / (float)D + p.eps);
     }
-    const bool gains = (p.flags & FORGE_NORM_QK) && p.qw;
-    const bool rope = (p.flags & FORGE_ROPE) && valid;
-    const float* cr = p.cos + b * p.csb + t * p.cst;
-    const float* sr = p.sin + b * p.csb + t * p.cst;
+    const float* cr = tab + (1 + (t - tok_lo)) * D;
+    const float* sr = tab + (1 + TL::MAX_TOK + (t - tok_lo)) * D;
     // channels x..x+7 (step s) and their RoPE partners x + D/2 (step s + KSTEPS/2)
 #pragma unroll
     for (int s = 0; s < KSTEPS / 2; ++s) {
@@ -738,8 +794,8 @@ void verify_mfma_kernel(SplitParams p) {
       unpack16<T>(qraw[s + KSTEPS / 2], z);
       if (gains) {
         float wa[8], wz[8];
-        load_f32x8_any(p.qw + x, wa, p.vec_tables);
-        load_f32x8_any(p.qw + x + D / 2, wz, p.vec_tables);
+        load_f32x8(tab + x, wa);
+        load_f32x8(tab + x + D / 2, wz);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           a[e] = a[e] * rs * wa[e];
@@ -752,12 +808,12 @@ void verify_mfma_kernel(SplitParams p) {
           z[e] *= rs;
         }
       }
-      if (rope) {
+      if (rope && valid) {
         float c1[8], s1[8], c2[8], s2[8];
-        load_f32x8_any(cr + x, c1, p.vec_tables);
-        load_f32x8_any(sr + x, s1, p.vec_tables);
-        load_f32x8_any(cr + x + D / 2, c2, p.vec_tables);
-        load_f32x8_any(sr + x + D / 2, s2, p.vec_tables);
+        load_f32x8(cr + x, c1);
+        load_f32x8(sr + x, s1);
+        load_f32x8(cr + x + D / 2, c2);
+        load_f32x8(sr + x + D / 2, s2);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float a0 = a[e], z0 = z[e];
@@ -791,20 +847,30 @@ void verify_mfma_kernel(SplitParams p) {
   const float cl2 = p.scale_log2;
 
   for (int i = 0; i < ntiles; ++i) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's share of tile i landed
-    __syncthreads();                                  // every share; tile i-1's stage free
-    issue(i + 1);
+    // tile i has landed once at most the loads of the tiles issued after it remain
+    const int after = ntiles - 1 - i < TL::STAGES - 2 ? ntiles - 1 - i : TL::STAGES - 2;
+    if (after >= 2) vwait_vm<4 * TL::LOADS>();
+    else if (after == 1) vwait_vm<2 * TL::LOADS>();
+    else vwait_vm<0>();
+    __syncthreads();  // every wave's share; the stage of tile i - 1 is free
+    issue(i + TL::STAGES - 1);
     const int key0 = c0 + (t_first + i) * BN;
-    const char* kl = smem + (2 * (i & 1)) * TL::TILEB + k_rd;
-    const char* vl = smem + (2 * (i & 1) + 1) * TL::TILEB;
+    const char* kl = smem + (2 * (i % TL::STAGES)) * TL::TILEB + k_rd;
+    const char* vl = smem + (2 * (i % TL::STAGES) + 1) * TL::TILEB;
 
-    // S^T = K . Q^T for the 32 keys of the tile
-    v_floatx16 sacc;
+    // S^T = K . Q^T for the 32 keys of the tile: four accumulation chains over the k-steps
+    // (a chain of dependent MFMAs issues at half rate), added in a fixed order
+    v_floatx16 sc[4];
 #pragma unroll
-    for (int x = 0; x < 16; ++x) sacc[x] = 0.0f;
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) sc[j][x] = 0.0f;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
-      sacc = VMfma<T>::run(*reinterpret_cast<const V8*>(kl + (((2 * s + hi) ^ k_sw) << 4)), qreg[s], sacc);
+      sc[s & 3] = VMfma<T>::run(*reinterpret_cast<const V8*>(kl + (((2 * s + hi) ^ k_sw) << 4)), qreg[s], sc[s & 3]);
+    v_floatx16 sacc;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) sacc[x] = (sc[0][x] + sc[1][x]) + (sc[2][x] + sc[3][x]);
 
     // element x of this lane is key key0 + 8(x/4) + 4hi + x%4 of row n
     const int lo = kmin - key0 - 4 * hi, top = kmax - key0 - 4 * hi;
@@ -900,6 +966,13 @@ static bool head_dim_ok(int D) { return D == 32 || D == 64 || D == 128 || D == 2
 
 // The MFMA path (verify_mfma_kernel) serves bf16/fp16 head dim 128/256 with G >= 4 query
 // heads per KV head, whatever T is (so verify and decode of one model share it).
+// Blocks of the MFMA verify kernel one CU holds (its LDS, 160 KB per CU, is the limit).
+static int verify_blocks_per_cu(int D) {
+  const int lds = D == 256 ? VerifyTile<256>::LDS_BYTES : VerifyTile<128>::LDS_BYTES;
+  const int n = (160 * 1024) / lds;
+  return n < 1 ? 1 : (n > 2 ? 2 : n);
+}
+
 static bool use_verify_mfma(int dtype, int D, int G) {
   return dtype != FORGE_F32 && (D == 128 || D == 256) && G >= 4;
 }
@@ -918,15 +991,16 @@ static int auto_chunk(int dtype, int B, int /*T*/, int H, int K, int D, int64_t 
   const int G = H / K;
   if (use_verify_mfma(dtype, D, G)) {
     // The smallest multiple of 32 keys that puts every unit into one round of the device's
-    // block slots (two per CU): with one more unit than slots, the last few full units run
-    // as a second round and double the kernel's time. (rows of T = 1, as the module asks.)
+    // block slots (CUs x blocks per CU): with one more unit than slots, the last few full
+    // units run as a second round and double the kernel's time. (rows of T = 1, as the
+    // module asks.)
     const int64_t pairs = (int64_t)B * K * ((G * T + kVerifyRows - 1) / kVerifyRows);
     const int64_t len = max_kv_len > 0 ? max_kv_len : 1;
     int ncu = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
       ncu = 256;
-    const int64_t slots = 2 * (int64_t)ncu;
+    const int64_t slots = (int64_t)verify_blocks_per_cu(D) * ncu;
     const int64_t per_pair = slots / pairs > 1 ? slots / pairs : 1;  // chunks per (b, kv head, rows)
     int64_t chunk = (len + per_pair - 1) / per_pair;
     chunk = (chunk + 31) / 32 * 32;
