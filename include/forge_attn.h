@@ -97,7 +97,9 @@ int forge_kv_append(int dtype, int B, int T, int K, int D, const void* k, int64_
  * key's contribution does not depend on T, so a verify row equals the decode of that
  * token alone bit for bit when both use the same chunk (pass the chunk explicitly, or
  * the same max_kv_len, to guarantee that).
- * workspace: device memory of forge_attn_decode_workspace_bytes(...) bytes.
+ * workspace: device memory of forge_attn_decode_workspace_bytes(...) bytes (fp32 split-K
+ * partials, and a work counter that the call zeroes on its own stream before use); calls
+ * that may run at the same time need separate workspaces.
  */
 int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, const void* q,
                       int64_t sqb, int64_t sqh, int64_t sqt, const float* q_weight, float eps,

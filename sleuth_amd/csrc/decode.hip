@@ -73,6 +73,7 @@ struct SplitParams {
   int vec_tables; // 1: cos/sin rows and q gains are 16-byte aligned (vector loads)
   float2* ws_ml;  // [B*H*T][max_chunks] (m, l)
   float* ws_o;    // [B*H*T][max_chunks][D]
+  int* ws_ctr;    // work ticket of the persistent grid (zeroed before each launch), or null
 };
 
 // Eight fp32 values: two 16-byte loads when the caller's tables allow it (a block-uniform
@@ -202,7 +203,8 @@ template <int D, int ROWS> struct SplitShared {
 // caller guarantees the block is converged (the unit may leave early, block-uniformly).
 template <typename T, int D, int ROWS>
 __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, const int kvh,
-                                           const int rb, const int c, SplitShared<D, ROWS>& sh) {
+                                           const int rb, const int c, SplitShared<D, ROWS>& sh,
+                                           int* ticket = nullptr) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int LPR = D / VEC;  // lanes per key row
   static_assert(LPR >= 2 && LPR <= kWave && (LPR & (LPR - 1)) == 0, "bad head dim");
@@ -238,7 +240,10 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
     }
   }
   const int c0 = c * p.chunk;
-  if (c0 > kmax_rb || c0 + p.chunk - 1 < kmin_rb) return;  // block-uniform
+  if (c0 > kmax_rb || c0 + p.chunk - 1 < kmin_rb) {  // block-uniform
+    if (ticket && tid == 0) *ticket = (int)gridDim.x + atomicAdd(p.ws_ctr, 1);
+    return;
+  }
   const int iters = p.chunk / KPI;
   int it_first = kmin_rb > c0 ? (kmin_rb - c0) / KPI : 0;
   int it_last = (kmax_rb - c0) / KPI;
@@ -271,6 +276,9 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
 #pragma unroll
   for (int j = 0; j < PF - 1; ++j)
     if (it_first + j <= it_last) load_iter(it_first + j, kbuf[j], vbuf[j]);
+
+  // the persistent grid's next work ticket: its round trip hides under this unit
+  if (ticket && tid == 0) *ticket = (int)gridDim.x + atomicAdd(p.ws_ctr, 1);
 
   uint4 q[ROWS];
 #pragma unroll
@@ -426,10 +434,12 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
 // memory): a fixed grid of about as many blocks as
 // the GPU holds at once; every block derives the per-row chunk ranges from the device
 // positions (so the launch needs no host knowledge of ragged lengths and stays
-// graph-safe), builds the prefix sum of work units per batch row in LDS, and walks the
-// units u = blockIdx.x, blockIdx.x + gridDim.x, ... Units are ordered (row b, KV head x
-// row block, chunk) with the chunk fastest, so the units in flight stream neighbouring
-// chunks of a few (b, kv head) slabs, and no block is spent on chunks past a row's end.
+// graph-safe), builds the prefix sum of work units per batch row in LDS, and takes units
+// by ticket from a counter in the workspace (zeroed by a one-thread kernel launched just
+// before): blocks on CUs that stream faster take more units, so all blocks finish
+// together. Units are ordered (row b, KV head x row block, chunk) with the chunk fastest,
+// so the units in flight stream neighbouring chunks of a few (b, kv head) slabs, and no
+// block is spent on chunks past a row's end.
 // Grid mode (batches too large for the LDS prefix): one block per (chunk, head x row
 // block, batch row), as before.
 constexpr int kPersistMaxRows = 2048;
@@ -487,7 +497,13 @@ void splitk_kernel(SplitParams p) {
   }
   __syncthreads();
   const int total = sh_pref[p.B];
-  for (int u = blockIdx.x; u < total; u += gridDim.x) {
+  // Block i starts with unit i; after that units go by ticket (grid + an atomic counter
+  // in the workspace, which the host zeroes before the launch), so a block on a CU that
+  // streams faster takes more of them. A block fetches its next ticket when it starts a
+  // unit and reads it after the unit's merge.
+  __shared__ int sh_ticket;
+  for (int u = blockIdx.x; u < total; u = sh_ticket) {
+    int next = total;
     int lo = 0, hi = p.B - 1;  // last row with sh_pref[row] <= u
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -497,9 +513,16 @@ void splitk_kernel(SplitParams p) {
     const int o = u - sh_pref[lo];
     const int n = sh_nch[lo];
     const int pr = o / n;
-    split_unit<T, D, ROWS>(p, lo, pr % p.K, pr / p.K, sh_cmin[lo] + o % n, sh);
-    __syncthreads();  // the next unit reuses the merge LDS
+    split_unit<T, D, ROWS>(p, lo, pr % p.K, pr / p.K, sh_cmin[lo] + o % n, sh, &next);
+    if (tid == 0) sh_ticket = next;
+    __syncthreads();  // the next unit reuses the merge LDS; the ticket is visible
   }
+}
+
+// Zeroes the work ticket of the next persistent launch on this stream (a kernel rather
+// than a memset, so that the call can be captured into a graph).
+__global__ void ticket_reset_kernel(int* ctr) {
+  if (threadIdx.x == 0) ctr[0] = 0;
 }
 
 // One block (4 waves) per (b, h, t) row: wave w merges chunks w, w+4, ... of the row
@@ -1057,7 +1080,7 @@ static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
   // position the dense grid has no such blocks, and the hardware's dynamic block dispatch
   // balances uneven per-CU bandwidth better than a fixed assignment does.
   const bool device_lengths = p.row_pos != nullptr || p.pos_dev != nullptr;
-  if (device_lengths && p.B <= kPersistMaxRows) {
+  if (device_lengths && p.B <= kPersistMaxRows && p.ws_ctr) {
     const int64_t upper = (int64_t)p.B * p.K * n_rb * p.max_chunks;
     int blocks = resident_blocks(kern);
     if (blocks <= 0) return set_error("forge_attn_decode: cannot query the device");
@@ -1066,6 +1089,9 @@ static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
       return set_error("forge_attn_decode: too many work units");
     p.persist = 1;
     grid = dim3((unsigned)blocks);
+    hipLaunchKernelGGL(ticket_reset_kernel, dim3(1), dim3(64), 0, s, p.ws_ctr);
+    const int st0 = check_launch();
+    if (st0) return st0;
   } else {
     if ((int64_t)p.K * n_rb > 65535 || p.B > 65535) return set_error("grid too large");
     p.persist = 0;
@@ -1141,7 +1167,8 @@ extern "C" size_t forge_attn_decode_workspace_bytes(int dtype, int B, int T, int
   if (max_chunks < 2) return 0;
   const int64_t slots = (int64_t)B * H * T * max_chunks;
   const size_t ml = ((size_t)slots * sizeof(float2) + 255) / 256 * 256;
-  return ml + (size_t)slots * D * sizeof(float);
+  const size_t o = ((size_t)slots * D * sizeof(float) + 255) / 256 * 256;
+  return ml + o + 256;  // + the persistent grid's work ticket
 }
 
 extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, const void* q,
@@ -1223,6 +1250,8 @@ extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, c
     const size_t ml = ((size_t)slots * sizeof(float2) + 255) / 256 * 256;
     p.ws_ml = static_cast<float2*>(workspace);
     p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + ml);
+    const size_t o = ((size_t)slots * D * sizeof(float) + 255) / 256 * 256;
+    p.ws_ctr = reinterpret_cast<int*>(static_cast<char*>(workspace) + ml + o);
   }
   const int rows = rows_per_block(p.rows_total);
   hipStream_t s = (hipStream_t)stream;
