@@ -58,9 +58,9 @@ class DecodeWorkload:
         # norm gains: bf16 parameters, held in fp32 by the caller (converted once, like the module)
         self.wq = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(dtype).float()
         self.wk = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(dtype).float()
-        import oracle  # RoPE tables only (the same fp32 formula the model buffers use)
+        from sleuth_amd.rope import rope_tables  # the tables the model's buffers hold
 
-        cos, sin = oracle.rope_tables(D, self.max_len + T, theta)
+        cos, sin = rope_tables(D, self.max_len + T, theta)
         base = torch.tensor([L - T for L in lens])
         idx = base[:, None] + torch.arange(T)[None, :]
         self.cos = cos[idx].to(dev)
@@ -133,9 +133,9 @@ class PrefillWorkload:
         self.v = torch.randn(B, T, K, D, generator=g, device=dev, dtype=dtype).transpose(1, 2)
         self.wq = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(dtype).float()
         self.wk = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(dtype).float()
-        import oracle
+        from sleuth_amd.rope import rope_tables
 
-        cos, sin = oracle.rope_tables(D, T, theta)
+        cos, sin = rope_tables(D, T, theta)
         self.cos, self.sin = cos.to(dev), sin.to(dev)
         self.kc = torch.zeros(B, K, T, D, device=dev, dtype=dtype)
         self.vc = torch.zeros_like(self.kc)
@@ -161,6 +161,11 @@ class PrefillWorkload:
     def flops(self) -> float:
         """4 * hd * sum over (b, h, query) of the keys it sees (causal: T(T+1)/2)."""
         return 4.0 * self.D * self.B * self.H * self.T * (self.T + 1) / 2
+
+    def flops_full_s(self) -> float:
+        """The reference's attention FLOP convention (flops.py:84-89, forward third of its
+        12*H*hd*S training term): 4 * H * hd * S per token with S = T, no causal halving."""
+        return 4.0 * self.D * self.H * self.T * self.B * self.T
 
 
 # ----------------------------------------------------------------------------- timing
@@ -365,6 +370,10 @@ def main() -> int:
         "decode_tokens_per_s": round(tok_s, 1),
         "decode_attention_call_us": round(t_attn * 1e6, 2),
         "prefill_tflops": round(p_tflops, 1),
+        # the reference's convention (sleuth/forge/model/flops.py:84-89): 4*H*hd*S FLOPs per
+        # token forward with S the full 4096, i.e. twice the causal count above; for
+        # comparison only (the roofline fraction uses the causal count)
+        "prefill_tflops_full_s_convention": round(p_tflops * pf.flops_full_s() / pf.flops(), 1),
         "prefill_step_ms": round(t_pstep * 1e3, 4),
         "prefill_config": "C3: 4 x 4096 causal, 16 q / 8 kv heads, head dim 128, bf16, QK-norm, RoPE theta 1e6",
         "roofline": {"bound": "hbm", "kernel": "forge::splitk_kernel + combine_kernel (one forge_attn_decode call)",

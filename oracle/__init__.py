@@ -12,6 +12,7 @@ from .attention_ref import (  # noqa: F401
     attention_forward,
     attention_mask,
     brute_attention,
+    drafter_attention,
     explicit_attention,
     head_norm_rope,
     ragged_decode,

@@ -181,6 +181,21 @@ def ragged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     return out
 
 
+def drafter_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                      n_past: int, window: int, scale: float = 1.0) -> torch.Tensor:
+    """The MTP drafter's attention onto the target's cache (infer/mtp.py:73-92,
+    AssistantLayer.forward with mask=None): the first n_past cached keys, and for a
+    sliding layer with n_past > window - 1 only the last window - 1 of them (mtp.py:84-86),
+    then SDPA with scale 1.0 and GQA (mtp.py:87-88). q [B,H,1,hd] -> [B,H,1,hd]."""
+    k, v = k_cache[:, :, :n_past], v_cache[:, :, :n_past]
+    if window and n_past > window - 1:
+        k, v = k[:, :, n_past - (window - 1):], v[:, :, n_past - (window - 1):]
+    kw = {"scale": scale}
+    if k.shape[1] != q.shape[1]:
+        kw["enable_gqa"] = True
+    return F.scaled_dot_product_attention(q, k.to(q.dtype), v.to(q.dtype), **kw)
+
+
 # ----------------------------------------------------------------------------- caches
 class KVCache:
     """kv_cache.py:25-70: per-layer k/v [B, K, max_len, hd] zeros, one shared `pos`;

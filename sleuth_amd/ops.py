@@ -221,6 +221,32 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *
     return out
 
 
+def attn_drafter(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *,
+                 n_past: int | None = None, n_past_dev: torch.Tensor | None = None,
+                 window: int = 0, scale: float = 1.0, **kw) -> torch.Tensor:
+    """The MTP drafter's attention onto the target's cache (sleuth/forge/infer/mtp.py:73-92,
+    and its graph form with the position on the device, mtp.py:169-188): one query per
+    row, at position n_past, over the n_past keys the target has stored (positions
+    0 .. n_past-1); with a sliding window only keys k with n_past - k < window (llama.cpp's
+    rule, mtp.py:84-86). Scale 1.0 by default. This is forge_attn_decode with the query
+    placed at n_past - 1 (so it sees keys up to n_past - 1) and the window narrowed by
+    one. q [B,H,1,D] (normalised and rotated by the drafter, or raw with norm_q/cos/sin
+    as for attn_decode); returns [B,1,H,D]."""
+    if q.shape[2] != 1:
+        raise ValueError("the drafter attends with one query per row")
+    if window < 0 or window == 1:
+        raise ValueError("window must be 0 (global) or at least 2")
+    w = window - 1 if window else 0
+    if n_past_dev is not None:
+        if n_past is not None:
+            raise ValueError("give n_past or n_past_dev, not both")
+        return attn_decode(q, k_cache, v_cache, scale=scale, pos_dev=n_past_dev.to(torch.int64) - 1,
+                           window=w, **kw)
+    if n_past is None or int(n_past) < 1:
+        raise ValueError("n_past must be at least 1: the drafter needs keys the target stored")
+    return attn_decode(q, k_cache, v_cache, scale=scale, pos=int(n_past) - 1, window=w, **kw)
+
+
 PREFILL_HEAD_DIMS = (64, 128, 256)
 
 
@@ -266,4 +292,4 @@ def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: fl
 
 
 __all__ = ["head_norm_rope", "kv_append", "attn_decode", "attn_prefill", "decode_chunk",
-           "decode_workspace_bytes", "prefill_supported", "dtype_code", "_lib"]
+           "decode_workspace_bytes", "attn_drafter", "prefill_supported", "dtype_code", "_lib"]

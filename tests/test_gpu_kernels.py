@@ -197,6 +197,35 @@ def test_decode_pos_dev_matches_host_pos(H, K):
     assert torch.equal(a, b)
 
 
+# ------------------------------------------------------------------ MTP drafter attention
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("H,K,D", [(8, 2, 128), (8, 1, 256)])
+@pytest.mark.parametrize("n_past,window", [(1, 0), (300, 0), (1000, 0), (200, 512), (900, 512), (512, 512)])
+def test_drafter_attention(dtype, H, K, D, n_past, window):
+    """The drafter's query at position n_past over the target's stored keys (mtp.py:73-92),
+    host position and device position (the graph form, mtp.py:169-188)."""
+    g = gen(400 + n_past + window)
+    B, L = 2, 1024
+    q = randn(g, B, H, 1, D, dtype=dtype)
+    kc = randn(g, B, K, L, D, dtype=dtype)
+    vc = randn(g, B, K, L, D, dtype=dtype)
+    ref = oracle.drafter_attention(q.float(), kc.float(), vc.float(), n_past, window, 1.0 / 16)
+    got = ops().attn_drafter(q.to(DEV), kc.to(DEV), vc.to(DEV), n_past=n_past, window=window, scale=1.0 / 16)
+    assert max_abs(got.cpu().transpose(1, 2), ref) <= tol(dtype)
+    got_dev = ops().attn_drafter(q.to(DEV), kc.to(DEV), vc.to(DEV), n_past_dev=torch.tensor([n_past], device=DEV),
+                                 window=window, scale=1.0 / 16)
+    assert torch.equal(got_dev, got)
+
+
+def test_drafter_attention_rejects_bad_positions():
+    q = torch.zeros(1, 4, 1, 64, device=DEV, dtype=torch.bfloat16)
+    c = torch.zeros(1, 2, 16, 64, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        ops().attn_drafter(q, c, c, n_past=0)
+    with pytest.raises(ValueError):
+        ops().attn_drafter(q, c, c, n_past=4, window=1)
+
+
 # ------------------------------------------------------------------ MFMA prefill
 def _prefill_case(seed, dtype, B, H, K, D, T, offset, window, theta=1e4):
     g = gen(seed)

@@ -302,6 +302,33 @@ def test_golden_fixtures():
         np.testing.assert_allclose(got.double().numpy(), c["out"], atol=1e-5, err_msg=str(c["name"]))
 
 
+def check_drafter(fn) -> None:
+    """The drafter's key set, stated independently of the slicing in mtp.py:84-86: the query
+    at position n_past sees stored keys k < n_past with n_past - k < window (window 0: all),
+    checked by a float64 loop."""
+    g = torch.Generator().manual_seed(31)
+    B, H, K, D, L = 2, 4, 2, 16, 40
+    q = torch.randn(B, H, 1, D, generator=g)
+    kc = torch.randn(B, K, L, D, generator=g)
+    vc = torch.randn(B, K, L, D, generator=g)
+    for n_past, window in [(1, 0), (7, 0), (L, 0), (5, 8), (7, 8), (8, 8), (9, 8), (L, 8), (L, 2)]:
+        got = fn(q, kc, vc, n_past, window, 1.0).double()
+        want = torch.zeros(B, H, 1, D, dtype=torch.float64)
+        for b in range(B):
+            for h in range(H):
+                kh = h // (H // K)
+                keys = [k for k in range(n_past) if window == 0 or n_past - k < window]
+                s = torch.tensor([float((q[b, h, 0].double() * kc[b, kh, k].double()).sum()) for k in keys],
+                                 dtype=torch.float64)
+                w = torch.softmax(s, 0)
+                want[b, h, 0] = (w[:, None] * vc[b, kh, keys].double()).sum(0)
+        np.testing.assert_allclose(got.numpy(), want.numpy(), atol=1e-5, err_msg=str((n_past, window)))
+
+
+def test_drafter_attention_pinned():
+    check_drafter(oracle.drafter_attention)
+
+
 # ----------------------------------------------------------------------------- planted mistakes
 def _raises(check, fn):
     with pytest.raises(AssertionError):
@@ -339,3 +366,6 @@ def test_pins_catch_planted_mistakes():
     # attention: scale applied twice / window ignored
     _raises(check_attention, lambda q, k, v, off, win, sc: ref.sdpa(q, k, v, off, win, sc * sc))
     _raises(check_attention, lambda q, k, v, off, win, sc: ref.sdpa(q, k, v, off, 0, sc))
+    # drafter: the query's own position counted as stored / the window one key wider
+    _raises(check_drafter, lambda q, k, v, n, win, sc: ref.drafter_attention(q, k, v, min(n + 1, k.shape[2]), win, sc))
+    _raises(check_drafter, lambda q, k, v, n, win, sc: ref.drafter_attention(q, k, v, n, win + 1 if win else 0, sc))
