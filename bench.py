@@ -308,9 +308,10 @@ def main() -> int:
     ap.add_argument("--extra", action="store_true", help="also print lines for configs C2, C3-decode, C5")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--config", default="", help="with --only extra: run only the configs whose name contains this")
-    ap.add_argument("--only", choices=["decode", "prefill", "copy", "extra"],
+    ap.add_argument("--only", choices=["decode", "prefill", "copy", "gemm", "extra"],
                     help="time one workload (for rocprofv3 runs); copy = a 1 GiB torch copy, the "
-                         "known-size kernel that calibrates the HBM byte counters")
+                         "known-size kernel that calibrates the HBM byte counters; gemm = a bf16 "
+                         "library GEMM, the practical MFMA rate beside the vendor peak")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the attention hot path runs on a single MI355X here "
@@ -348,6 +349,8 @@ def main() -> int:
     p_tflops = pf.flops() / t_pattn / 1e12
     print(f"[bench] C3 prefill step {t_pstep * 1e6:.1f} us, attention kernel {t_pattn * 1e6:.1f} us "
           f"({p_tflops:.0f} TFLOP/s)", file=sys.stderr, flush=True)
+    gemm = gemm_tflops(dev)
+    print(f"[bench] bf16 8192^3 library GEMM {gemm:.0f} TFLOP/s", file=sys.stderr, flush=True)
 
     line = {
         "metric": METRIC,
@@ -384,7 +387,9 @@ def main() -> int:
         "roofline_prefill": {"bound": "mfma", "kernel": "forge::prefill_kernel<bf16,128>",
                              "achieved": round(p_tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(p_tflops / BF16_PEAK_TFLOPS, 4),
-                             "traffic": read_traffic("prefill_c3_traffic"), "flops": pf.flops()},
+                             "traffic": read_traffic("prefill_c3_traffic"), "flops": pf.flops(),
+                             "library_gemm_tflops": round(gemm, 1),
+                             "frac_of_library_gemm": round(p_tflops / gemm, 4)},
     }
     if not args.no_cpu:
         print("[bench] CPU baseline (decode sample) ...", file=sys.stderr, flush=True)
@@ -397,6 +402,17 @@ def main() -> int:
         line["extra"] = extra_configs(dev, args)
     print(json.dumps(line), flush=True)
     return 0
+
+
+def gemm_tflops(dev, n: int = 8192, steps: int = 20, warmup: int = 5) -> float:
+    """bf16 n x n x n torch.matmul (hipBLASLt on ROCm), in TFLOP/s: what a tuned library GEMM
+    reaches on this GPU, reported beside the 2.5 PFLOP/s vendor figure the roofline uses."""
+    g = torch.Generator(device=dev).manual_seed(0)
+    a = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=g)
+    b = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=g)
+    c = torch.empty(n, n, device=dev, dtype=torch.bfloat16)
+    t = time_loop(lambda: torch.matmul(a, b, out=c), steps, warmup)
+    return 2.0 * n ** 3 / t / 1e12
 
 
 def run_only(args, dev) -> int:
@@ -413,6 +429,9 @@ def run_only(args, dev) -> int:
         print(json.dumps({"workload": "C3 prefill step", "us": round(t * 1e6, 2)}), flush=True)
     elif args.only == "extra":
         print(json.dumps(extra_configs(dev, args)), flush=True)
+    elif args.only == "gemm":
+        print(json.dumps({"workload": "bf16 8192^3 torch.matmul", "TFLOPs": round(gemm_tflops(dev), 1)}),
+              flush=True)
     else:
         n = 1 << 30
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
