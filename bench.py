@@ -30,6 +30,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, TFLOP/s
 N_LAYERS = 28                # Qwen3-0.6B: tokens/s counts 28 layers per token
+PREFILL_WARM_S = 0.1         # untimed back-to-back calls before an MFMA-bound timing
 METRIC = "decode attn HBM GB/s + tokens/s (bs64, 32k ctx); prefill bf16 TFLOPS at 4k"
 
 
@@ -182,6 +183,21 @@ def time_loop(fn, steps: int, warmup: int) -> float:
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / 1e3 / steps
+
+
+def warm(fn, seconds: float = PREFILL_WARM_S) -> int:
+    """Runs fn back to back for about `seconds` of GPU time before a timing: an MFMA-heavy
+    kernel only reaches its steady clock after some tens of milliseconds of load (C3 prefill
+    on MI355X: about 355 us per call in the first 20 calls, 290 us from about the 60th on).
+    Returns the number of calls made."""
+    calls = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn()
+        calls += 8
+        torch.cuda.synchronize()
+    return calls
 
 
 def time_graph(fn, n: int, replays: int, warmup: int) -> float:
@@ -344,6 +360,7 @@ def main() -> int:
     # ---- C3 prefill
     pf = PrefillWorkload(4, 4096, 16, 8, 128, 1e6, dt, dev)
     pf.append()
+    warm(pf.step)
     t_pstep = time_loop(pf.step, max(3, args.steps // 2), max(1, args.warmup // 2))
     t_pattn = time_loop(pf.attend, max(3, args.steps // 2), max(1, args.warmup // 2))
     p_tflops = pf.flops() / t_pattn / 1e12
@@ -378,6 +395,7 @@ def main() -> int:
         # comparison only (the roofline fraction uses the causal count)
         "prefill_tflops_full_s_convention": round(p_tflops * pf.flops_full_s() / pf.flops(), 1),
         "prefill_step_ms": round(t_pstep * 1e3, 4),
+        "prefill_warm_s": PREFILL_WARM_S,
         "prefill_config": "C3: 4 x 4096 causal, 16 q / 8 kv heads, head dim 128, bf16, QK-norm, RoPE theta 1e6",
         "roofline": {"bound": "hbm", "kernel": "forge::splitk_kernel + combine_kernel (one forge_attn_decode call)",
                      "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -411,6 +429,7 @@ def gemm_tflops(dev, n: int = 8192, steps: int = 20, warmup: int = 5) -> float:
     a = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=g)
     b = torch.randn(n, n, device=dev, dtype=torch.bfloat16, generator=g)
     c = torch.empty(n, n, device=dev, dtype=torch.bfloat16)
+    warm(lambda: torch.matmul(a, b, out=c))
     t = time_loop(lambda: torch.matmul(a, b, out=c), steps, warmup)
     return 2.0 * n ** 3 / t / 1e12
 
@@ -425,6 +444,7 @@ def run_only(args, dev) -> int:
                           "GBs": round(wl.step_bytes() / t / 1e9, 1)}), flush=True)
     elif args.only == "prefill":
         pf = PrefillWorkload(4, 4096, 16, 8, 128, 1e6, torch.bfloat16, dev)
+        warm(pf.step)
         t = time_loop(pf.step, args.steps, args.warmup)
         print(json.dumps({"workload": "C3 prefill step", "us": round(t * 1e6, 2)}), flush=True)
     elif args.only == "extra":
