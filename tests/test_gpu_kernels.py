@@ -197,6 +197,29 @@ def test_decode_pos_dev_matches_host_pos(H, K):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("B", [8, 300])
+def test_persistent_grid_equals_dense_grid_bitwise(B):
+    """The persistent grid (device positions, units taken by ticket in any order) equals the
+    dense grid of host positions bit for bit, with few rows and with many."""
+    g = gen(21)
+    H, K, D, T, L = 4, 2, 64, 1, 700
+    kc = randn(g, B, K, 768, D, dtype=torch.bfloat16).to(DEV)
+    vc = randn(g, B, K, 768, D, dtype=torch.bfloat16).to(DEV)
+    q = randn(g, B, H, T, D, dtype=torch.bfloat16).to(DEV)
+    a = ops().attn_decode(q, kc, vc, scale=0.1, pos=L - T, chunk=128)
+    rp = torch.full((B,), L - T, dtype=torch.int32, device=DEV)
+    b = ops().attn_decode(q, kc, vc, scale=0.1, row_pos=rp, max_kv_len=768, chunk=128)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("B", [40, 300])
+def test_decode_ragged_many_rows(B):
+    """Ragged lengths over many rows of the persistent grid."""
+    lens = torch.randint(1, 700, (B,), generator=torch.Generator().manual_seed(B)).tolist()
+    got, ref = _decode_case(31, torch.bfloat16, B, 4, 2, 64, 1, lens, 0, chunk=128)
+    assert max_abs(got, ref) <= 2e-2
+
+
 # ------------------------------------------------------------------ MTP drafter attention
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("H,K,D", [(8, 2, 128), (8, 1, 256)])
