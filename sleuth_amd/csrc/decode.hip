@@ -1027,7 +1027,13 @@ static int auto_chunk(int dtype, int B, int /*T*/, int H, int K, int D, int64_t 
     const int64_t per_pair = slots / pairs > 1 ? slots / pairs : 1;  // chunks per (b, kv head, rows)
     int64_t chunk = (len + per_pair - 1) / per_pair;
     chunk = (chunk + 31) / 32 * 32;
-    return (int)(chunk < 32 ? 32 : chunk);
+    // At least as many tiles as the pipeline keeps in flight: a shorter unit cannot use its
+    // prefetch and is mostly prologue (C5 window 1024: 64-key chunks 23.2 us, 96-key 20.9 us).
+    constexpr int kMinTiles = VerifyTile<128>::STAGES - 1;
+    static_assert(VerifyTile<128>::STAGES == VerifyTile<256>::STAGES &&
+                  VerifyTile<128>::BN == VerifyTile<256>::BN, "one tile shape for both head dims");
+    const int64_t min_chunk = (int64_t)kMinTiles * VerifyTile<128>::BN;
+    return (int)(chunk < min_chunk ? min_chunk : chunk);
   }
   const int rows = rows_per_block(G * T);
   const int64_t n_rb = (G * T + rows - 1) / rows;
