@@ -324,10 +324,11 @@ def main() -> int:
     ap.add_argument("--extra", action="store_true", help="also print lines for configs C2, C3-decode, C5")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--config", default="", help="with --only extra: run only the configs whose name contains this")
-    ap.add_argument("--only", choices=["decode", "prefill", "copy", "gemm", "extra"],
+    ap.add_argument("--only", choices=["decode", "prefill", "copy", "gemm", "sdpa", "extra"],
                     help="time one workload (for rocprofv3 runs); copy = a 1 GiB torch copy, the "
                          "known-size kernel that calibrates the HBM byte counters; gemm = a bf16 "
-                         "library GEMM, the practical MFMA rate beside the vendor peak")
+                         "library GEMM, the practical MFMA rate beside the vendor peak; sdpa = torch's "
+                         "SDPA (the reference's GPU attention call) on the C3 shapes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the attention hot path runs on a single MI355X here "
@@ -368,6 +369,8 @@ def main() -> int:
           f"({p_tflops:.0f} TFLOP/s)", file=sys.stderr, flush=True)
     gemm = gemm_tflops(dev)
     print(f"[bench] bf16 8192^3 library GEMM {gemm:.0f} TFLOP/s", file=sys.stderr, flush=True)
+    sdpa = sdpa_reference(dev)
+    print(f"[bench] torch SDPA on the same GPU: {sdpa}", file=sys.stderr, flush=True)
 
     line = {
         "metric": METRIC,
@@ -397,6 +400,9 @@ def main() -> int:
         "prefill_step_ms": round(t_pstep * 1e3, 4),
         "prefill_warm_s": PREFILL_WARM_S,
         "prefill_config": "C3: 4 x 4096 causal, 16 q / 8 kv heads, head dim 128, bf16, QK-norm, RoPE theta 1e6",
+        # the reference's own GPU attention call (torch SDPA, flash / memory-efficient backends)
+        # on the same GPU and the C3 shapes, attention only
+        "torch_sdpa_same_gpu": sdpa,
         "roofline": {"bound": "hbm", "kernel": "forge::splitk_kernel + combine_kernel (one forge_attn_decode call)",
                      "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
@@ -434,6 +440,50 @@ def gemm_tflops(dev, n: int = 8192, steps: int = 20, warmup: int = 5) -> float:
     return 2.0 * n ** 3 / t / 1e12
 
 
+def sdpa_reference(dev, steps: int = 10, warmup: int = 3) -> dict:
+    """torch's scaled_dot_product_attention, the call the reference makes on the GPU
+    (attention.py:187-191), on the C3 shapes, timed like the kernels here. Only the flash and
+    memory-efficient backends are allowed (no math fallback); K/V heads are repeated to H
+    (attention.py:181-182) so that no GQA path is involved. Attention only: the reference's
+    norm, RoPE and cache update are not in the timing."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    g = torch.Generator(device=dev).manual_seed(3)
+    bf = torch.bfloat16
+    out = {}
+    backends = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
+    # C3 prefill: 4 x 4096 causal, 16 heads (8 KV heads repeated), head dim 128
+    B, T, H, D = 4, 4096, 16, 128
+    q = torch.randn(B, H, T, D, device=dev, dtype=bf, generator=g)
+    k = torch.randn(B, H // 2, T, D, device=dev, dtype=bf, generator=g).repeat_interleave(2, 1)
+    v = torch.randn(B, H // 2, T, D, device=dev, dtype=bf, generator=g).repeat_interleave(2, 1)
+    fn = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=D ** -0.5)
+    try:
+        with sdpa_kernel(backends):
+            warm(fn)
+            t = time_loop(fn, steps, warmup)
+        flops = 4 * D * H * B * (T * (T + 1) / 2)
+        out["C3_prefill"] = {"us": round(t * 1e6, 2), "TFLOPs": round(flops / t / 1e12, 1)}
+    except RuntimeError as e:
+        out["C3_prefill"] = {"error": str(e)[:200]}
+    del q, k, v
+    # C3 decode: 32 rows at 8192 keys, one query each
+    B, S = 32, 8192
+    q = torch.randn(B, H, 1, D, device=dev, dtype=bf, generator=g)
+    k = torch.randn(B, H // 2, S, D, device=dev, dtype=bf, generator=g).repeat_interleave(2, 1)
+    v = torch.randn(B, H // 2, S, D, device=dev, dtype=bf, generator=g).repeat_interleave(2, 1)
+    fn = lambda: F.scaled_dot_product_attention(q, k, v, scale=D ** -0.5)
+    try:
+        with sdpa_kernel(backends):
+            t = time_loop(fn, steps * 2, warmup)
+        kv_bytes = 2 * B * (H // 2) * S * D * 2  # the distinct K/V bytes a GQA kernel reads
+        out["C3_decode"] = {"us": round(t * 1e6, 2), "GBs_of_distinct_kv": round(kv_bytes / t / 1e9, 1)}
+    except RuntimeError as e:
+        out["C3_decode"] = {"error": str(e)[:200]}
+    return out
+
+
 def run_only(args, dev) -> int:
     """One workload's step loop and nothing else, for rocprofv3 runs."""
     if args.only == "decode":
@@ -449,6 +499,8 @@ def run_only(args, dev) -> int:
         print(json.dumps({"workload": "C3 prefill step", "us": round(t * 1e6, 2)}), flush=True)
     elif args.only == "extra":
         print(json.dumps(extra_configs(dev, args)), flush=True)
+    elif args.only == "sdpa":
+        print(json.dumps({"workload": "torch SDPA on the C3 shapes", **sdpa_reference(dev)}), flush=True)
     elif args.only == "gemm":
         print(json.dumps({"workload": "bf16 8192^3 torch.matmul", "TFLOPs": round(gemm_tflops(dev), 1)}),
               flush=True)
