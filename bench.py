@@ -324,11 +324,12 @@ def main() -> int:
     ap.add_argument("--extra", action="store_true", help="also print lines for configs C2, C3-decode, C5")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--config", default="", help="with --only extra: run only the configs whose name contains this")
-    ap.add_argument("--only", choices=["decode", "prefill", "copy", "gemm", "sdpa", "extra"],
+    ap.add_argument("--only", choices=["decode", "prefill", "copy", "gemm", "sdpa", "qkv", "extra"],
                     help="time one workload (for rocprofv3 runs); copy = a 1 GiB torch copy, the "
                          "known-size kernel that calibrates the HBM byte counters; gemm = a bf16 "
                          "library GEMM, the practical MFMA rate beside the vendor peak; sdpa = torch's "
-                         "SDPA (the reference's GPU attention call) on the C3 shapes")
+                         "SDPA (the reference's GPU attention call) on the C3 shapes; qkv = the "
+                         "module's q/k/v projections, separate against fused")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the attention hot path runs on a single MI355X here "
@@ -501,6 +502,27 @@ def sdpa_reference(dev, steps: int = 10, warmup: int = 3) -> dict:
     return out
 
 
+def qkv_projection(dev, steps: int = 50, warmup: int = 10) -> dict:
+    """The attention module's q/k/v projections on the Qwen3-0.6B shapes (d_model 1024,
+    16 q / 8 kv heads of 128): three nn.Linear calls (the reference, attention.py:106-108)
+    against the module's one GEMM over the concatenated weights."""
+    from sleuth_amd.attention import Attention
+    from sleuth_amd.config import ModelConfig
+
+    cfg = ModelConfig(d_model=1024, n_heads=16, head_size=128, n_kv_heads=8, qk_norm=True,
+                      rope_theta=1e6, max_seq_len=8192)
+    att = Attention(cfg, 0).to(dev).to(torch.bfloat16).eval()
+    out = {}
+    with torch.no_grad():
+        for B, T in ((64, 1), (4, 4096)):
+            x = torch.randn(B, T, cfg.d_model, device=dev, dtype=torch.bfloat16)
+            sep = lambda: (att.q_proj(x), att.k_proj(x), att.v_proj(x))
+            fus = lambda: att._qkv_fused(x)
+            ts, tf = time_loop(sep, steps, warmup), time_loop(fus, steps, warmup)
+            out[f"B{B}_T{T}"] = {"separate_us": round(ts * 1e6, 1), "fused_us": round(tf * 1e6, 1)}
+    return out
+
+
 def run_only(args, dev) -> int:
     """One workload's step loop and nothing else, for rocprofv3 runs."""
     if args.only == "decode":
@@ -518,6 +540,8 @@ def run_only(args, dev) -> int:
         print(json.dumps(extra_configs(dev, args)), flush=True)
     elif args.only == "sdpa":
         print(json.dumps({"workload": "torch SDPA on the C3 shapes and C4 row by row", **sdpa_reference(dev)}), flush=True)
+    elif args.only == "qkv":
+        print(json.dumps({"workload": "q/k/v projections, Qwen3-0.6B shapes", **qkv_projection(dev)}), flush=True)
     elif args.only == "gemm":
         print(json.dumps({"workload": "bf16 8192^3 torch.matmul", "TFLOPs": round(gemm_tflops(dev), 1)}),
               flush=True)

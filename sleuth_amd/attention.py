@@ -81,6 +81,47 @@ class Attention(nn.Module):
         self.tap_pattern = Tap()
         self.tap_z = Tap()
         self.last_path = ""   # "hip-decode" | "hip-prefill" | "torch" (for tests and stats)
+        self._qkv_key = None  # identity of the weights the fused projection buffer holds
+        self._qkv_w = self._qkv_b = None
+
+    # ------------------------------------------------------------------ projections
+    def _qkv_fused(self, x: torch.Tensor) -> torch.Tensor | None:
+        """q_proj, k_proj and v_proj (attention.py:106-108) as one GEMM during GPU inference.
+        The weights are concatenated once into a [(H + 2K)·hd, d] buffer and the three
+        modules' weights (and biases) become views of it, so no second copy is kept. The
+        buffer is rebuilt when a weight is replaced, moved or modified in place (its storage,
+        dtype or version changes). Returns None where the separate projections run: on the
+        CPU, with autograd, and whenever a projection is not a plain nn.Linear or has hooks
+        (adapters, quantised layers and forward hooks see the same calls as in the reference)."""
+        if not x.is_cuda or torch.is_grad_enabled() or hip_disabled():
+            return None
+        mods = [self.q_proj, self.k_proj] + ([self.v_proj] if self.v_proj is not None else [])
+        if any(type(m) is not nn.Linear or m._forward_hooks or m._forward_pre_hooks for m in mods):
+            return None
+        if nn.modules.module._global_forward_hooks or nn.modules.module._global_forward_pre_hooks:
+            return None
+
+        def key():
+            return tuple((m.weight.data_ptr(), m.weight._version, m.weight.dtype,
+                          None if m.bias is None else (m.bias.data_ptr(), m.bias._version))
+                         for m in mods)
+
+        if self._qkv_key != key():
+            if any(m.weight.dtype != x.dtype or m.weight.device != x.device for m in mods):
+                return None
+            w = torch.cat([m.weight.detach() for m in mods], 0)
+            has_b = mods[0].bias is not None
+            b = torch.cat([m.bias.detach() for m in mods], 0) if has_b else None
+            off = 0
+            for m in mods:
+                n = m.weight.shape[0]
+                m.weight.data = w[off:off + n]
+                if has_b:
+                    m.bias.data = b[off:off + n]
+                off += n
+            self._qkv_w, self._qkv_b = w, b
+            self._qkv_key = key()
+        return F.linear(x, self._qkv_w, self._qkv_b)
 
     # ------------------------------------------------------------------ dispatch
     def _use_hip(self, q: torch.Tensor, cache, same_doc) -> bool:
@@ -100,9 +141,16 @@ class Attention(nn.Module):
     def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, cache=None,
                 same_doc=None) -> torch.Tensor:
         B, T, _ = x.shape
-        q = self.q_proj(x).view(B, T, self.n_heads, self.hd).transpose(1, 2)  # [B, H, T, hd]
-        k = self.k_proj(x).view(B, T, self.n_kv, self.hd).transpose(1, 2)     # [B, K, T, hd]
-        v = k if self.v_proj is None else self.v_proj(x).view(B, T, self.n_kv, self.hd).transpose(1, 2)
+        H, K, hd = self.n_heads, self.n_kv, self.hd
+        y = self._qkv_fused(x)
+        if y is not None:  # one GEMM; q, k, v are strided views of its rows
+            q = y[..., :H * hd].view(B, T, H, hd).transpose(1, 2)
+            k = y[..., H * hd:(H + K) * hd].view(B, T, K, hd).transpose(1, 2)
+            v = k if self.v_proj is None else y[..., (H + K) * hd:].view(B, T, K, hd).transpose(1, 2)
+        else:
+            q = self.q_proj(x).view(B, T, H, hd).transpose(1, 2)  # [B, H, T, hd]
+            k = self.k_proj(x).view(B, T, K, hd).transpose(1, 2)  # [B, K, T, hd]
+            v = k if self.v_proj is None else self.v_proj(x).view(B, T, K, hd).transpose(1, 2)
         if self._use_hip(q, cache, same_doc):
             y = self._forward_hip(q, k, v, cos, sin, cache)
         else:

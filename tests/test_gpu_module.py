@@ -280,3 +280,34 @@ def test_static_step_equals_normal_step_on_gpu():
         out = m(ids[:, 20:25], cache=st).logits[0]
         st.static = False
     assert max_abs(out, full[20:25]) <= 1e-4
+
+
+def test_fused_qkv_projection_matches_separate():
+    """On the GPU inference path q, k and v come from one GEMM over the concatenated
+    weights (the three projections of attention.py:106-108 as one call). The module's output
+    matches the separate projections' (a forward hook on a projection forces those), the
+    weights become views of one buffer, and an in-place weight update is picked up."""
+    Attention, ModelConfig, _ = _modules()
+    cfg = ModelConfig(vocab_size=10, d_model=256, n_heads=8, n_kv_heads=4, head_size=32, qk_norm=True,
+                      n_layers=1)
+    torch.manual_seed(0)
+    a = Attention(cfg, 0).eval().to(DEV, torch.bfloat16)
+    x = torch.randn(2, 5, 256, device=DEV, dtype=torch.bfloat16)
+    cos, sin = oracle.rope_tables(32, 16, 1e4)
+    cos, sin = cos[:5].to(DEV), sin[:5].to(DEV)
+
+    def separate():
+        h = a.q_proj.register_forward_hook(lambda m, i, o: None)
+        try:
+            return a(x, cos, sin)
+        finally:
+            h.remove()
+
+    with torch.no_grad():
+        fused = a(x, cos, sin)
+        assert a._qkv_w is not None and a.q_proj.weight.data_ptr() == a._qkv_w.data_ptr()
+        assert max_abs(fused.float().cpu(), separate().float().cpu()) <= 2e-2
+        a.k_proj.weight.mul_(2.0)
+        fused2 = a(x, cos, sin)
+        assert max_abs(fused2.float().cpu(), separate().float().cpu()) <= 2e-2
+        assert not torch.equal(fused2, fused)
