@@ -8,15 +8,17 @@ signature forward(x, cos, sin, cache=None, same_doc=None) -> [B, T, d].
 Paths (the reference's own dispatch, attention.py:109-153, with the HIP kernels in place
 of head_norm_rope + cache.update + SDPA):
   * HIP (GPU inference: no grad, dtype fp32/bf16/fp16, head dim 32/64/128/256, no
-    partial RoPE, no document mask, nobody listening on attn.pattern):
+    document mask, nobody listening on attn.pattern):
       forge_kv_append   k norm + RoPE (+ v norm), written into the cache at pos /
-                        pos_t / per-row lengths;
+                        pos_t / per-row lengths (with partial RoPE, norm and RoPE run in
+                        torch as the reference's eager code does, and the kernels take
+                        q and k as they are);
       T <= 16           forge_attn_decode (split-K; decode, verify, static steps), q norm
                         + RoPE fused into its q load;
       T > 16            forge_attn_prefill (bf16/fp16 MFMA flash, head dim 64/128/256)
                         else forge_attn_decode (fp32 and other head sizes).
     The output comes back as [B, T, H, hd], the layout o_proj reads.
-  * torch (CPU, training, partial RoPE, document masks, the pattern tap, or
+  * torch (CPU, training, document masks, the pattern tap, or
     SLEUTH_AMD_NO_HIP=1): the reference's eager code, unchanged in meaning.
 If a GPU tensor would take the HIP path and the library is missing or fails its
 first-use self-check, forward raises: there is no silent fallback.
@@ -129,7 +131,7 @@ class Attention(nn.Module):
             return False
         if torch.is_grad_enabled() and q.requires_grad:
             return False
-        if self.partial_rope or same_doc is not None or self.tap_pattern.active:
+        if same_doc is not None or self.tap_pattern.active:
             return False
         if q.dtype not in _HIP_DTYPES or self.hd not in _HIP_HEAD_DIMS:
             return False
@@ -170,7 +172,20 @@ class Attention(nn.Module):
             rc, rs = rc.float(), rs.float()
         qw = self.q_norm.weight_f32() if qn else None
         kw = self.k_norm.weight_f32() if kn else None
-        if self.tap_q.active or self.tap_k.active:
+        if self.partial_rope:
+            # RoPE over the first rope_dim channels only: the reference keeps this off its fused
+            # kernel (attention.py:109) and runs RMSNorm then apply_rope, each rounded to the
+            # dtype (attention.py:120-126, rope.py:46-55); so does this path, and the kernels
+            # take q and k as they are.
+            if qn:
+                q, k = self.q_norm(q), self.k_norm(k)
+            if self.use_rope:
+                c, s_ = (cos[:, None], sin[:, None]) if cos.dim() == 3 else (cos, sin)
+                q, k = apply_rope(q, c, s_), apply_rope(k, c, s_)
+            q, k = self.tap_q(q), self.tap_k(k)
+            q_args = dict(norm_q=False, cos=None, sin=None)
+            k_args = dict(norm_k=False, cos=None, sin=None)
+        elif self.tap_q.active or self.tap_k.active:
             # Listeners see (and may replace) q and k after RoPE: materialise them.
             if qn or rc is not None:
                 q = ops.head_norm_rope(q, qw, self.eps if qn else 0.0, rc, rs, qn)

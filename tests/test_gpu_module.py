@@ -311,3 +311,34 @@ def test_fused_qkv_projection_matches_separate():
         fused2 = a(x, cos, sin)
         assert max_abs(fused2.float().cpu(), separate().float().cpu()) <= 2e-2
         assert not torch.equal(fused2, fused)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_partial_rope_on_the_hip_path(dtype, monkeypatch):
+    """Partial RoPE (rope_dim < head dim, rope.py:46-55): norm and RoPE in torch as the
+    reference's eager path, attention and the cache write in the kernels. The outputs of a
+    40-token prefill and 3 decode steps match the torch path (SLEUTH_AMD_NO_HIP=1)."""
+    Attention, ModelConfig, KVCache = _modules()
+    cfg = ModelConfig(vocab_size=10, d_model=256, n_heads=4, n_kv_heads=2, head_size=64, qk_norm=True,
+                      rope_dim=32, n_layers=1)
+    torch.manual_seed(1)
+    a = Attention(cfg, 0).eval().to(DEV, dtype)
+    cos_t, sin_t = oracle.rope_tables(32, 64, 1e4)
+    outs = {}
+    for mode in ("hip", "torch"):
+        if mode == "torch":
+            monkeypatch.setenv("SLEUTH_AMD_NO_HIP", "1")
+        g = torch.Generator().manual_seed(2)
+        cache = KVCache([(2, 64)], 2, 64, DEV, dtype)
+        res = []
+        with torch.no_grad():
+            for T in (40, 1, 1, 1):
+                x = torch.randn(2, T, 256, generator=g).to(DEV, dtype)
+                p = cache.pos
+                res.append(a(x, cos_t[p:p + T].to(DEV), sin_t[p:p + T].to(DEV), cache).float().cpu())
+                assert a.last_path == ("torch" if mode == "torch" else
+                                       ("hip-prefill" if T > 16 and dtype != torch.float32 else "hip-decode"))
+                cache.advance(T)
+        outs[mode] = res
+    for got, ref in zip(outs["hip"], outs["torch"]):
+        assert max_abs(got, ref) <= (1e-4 if dtype == torch.float32 else 2e-2)
