@@ -313,32 +313,68 @@ def test_fused_qkv_projection_matches_separate():
         assert not torch.equal(fused2, fused)
 
 
+def _hip_against_cpu(mod, d_model, kv, cos_t, sin_t, seed, expect_hip):
+    """Runs mod on the GPU (HIP path) and a copy of it on the CPU (the reference's eager
+    path, so no reference attention runs on the GPU) over a 40-token prefill and 3 decode
+    steps through a cache; returns [(gpu_out, cpu_out)] per call."""
+    import copy
+
+    from sleuth_amd.kv_cache import KVCache
+
+    dtype = next(mod.parameters()).dtype
+    cpu = copy.deepcopy(mod).cpu()
+    outs = []
+    caches = {"gpu": KVCache([kv], 2, 64, DEV, dtype), "cpu": KVCache([kv], 2, 64, "cpu", dtype)}
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for T in (40, 1, 1, 1):
+            x = torch.randn(2, T, d_model, generator=g).to(dtype)
+            p = caches["gpu"].pos
+            c, s_ = cos_t[p:p + T], sin_t[p:p + T]
+            got = mod(x.to(DEV), c.to(DEV), s_.to(DEV), caches["gpu"]).float().cpu()
+            assert mod.last_path == expect_hip(T)
+            ref = cpu(x, c, s_, caches["cpu"]).float()
+            assert cpu.last_path == "torch"
+            outs.append((got, ref))
+            for cache in caches.values():
+                cache.advance(T)
+    return outs
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_partial_rope_on_the_hip_path(dtype, monkeypatch):
+def test_partial_rope_on_the_hip_path(dtype):
     """Partial RoPE (rope_dim < head dim, rope.py:46-55): norm and RoPE in torch as the
-    reference's eager path, attention and the cache write in the kernels. The outputs of a
-    40-token prefill and 3 decode steps match the torch path (SLEUTH_AMD_NO_HIP=1)."""
-    Attention, ModelConfig, KVCache = _modules()
+    reference's eager path, attention and the cache write in the kernels; the outputs match
+    the eager path run on the CPU."""
+    Attention, ModelConfig, _ = _modules()
     cfg = ModelConfig(vocab_size=10, d_model=256, n_heads=4, n_kv_heads=2, head_size=64, qk_norm=True,
                       rope_dim=32, n_layers=1)
     torch.manual_seed(1)
     a = Attention(cfg, 0).eval().to(DEV, dtype)
     cos_t, sin_t = oracle.rope_tables(32, 64, 1e4)
-    outs = {}
-    for mode in ("hip", "torch"):
-        if mode == "torch":
-            monkeypatch.setenv("SLEUTH_AMD_NO_HIP", "1")
-        g = torch.Generator().manual_seed(2)
-        cache = KVCache([(2, 64)], 2, 64, DEV, dtype)
-        res = []
-        with torch.no_grad():
-            for T in (40, 1, 1, 1):
-                x = torch.randn(2, T, 256, generator=g).to(DEV, dtype)
-                p = cache.pos
-                res.append(a(x, cos_t[p:p + T].to(DEV), sin_t[p:p + T].to(DEV), cache).float().cpu())
-                assert a.last_path == ("torch" if mode == "torch" else
-                                       ("hip-prefill" if T > 16 and dtype != torch.float32 else "hip-decode"))
-                cache.advance(T)
-        outs[mode] = res
-    for got, ref in zip(outs["hip"], outs["torch"]):
+    prefill = "hip-prefill" if dtype != torch.float32 else "hip-decode"
+    for got, ref in _hip_against_cpu(a, 256, (2, 64), cos_t, sin_t, 2,
+                                     lambda T: prefill if T > 16 else "hip-decode"):
+        assert max_abs(got, ref) <= (1e-4 if dtype == torch.float32 else 2e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gated_attention_hip_matches_torch(dtype):
+    """Qwen3.5 gated attention (qwen35.py:187-216): q/gate split, partial RoPE, sigmoid gate.
+    The kernels' cache write and attention match the reference's eager path (run on the CPU)."""
+    from types import SimpleNamespace
+
+    from sleuth_amd.gated import GatedAttention
+
+    cfg = SimpleNamespace(n_heads=4, n_kv_heads=2, head_dim=64, n_rot=32, norm_eps=1e-6)
+    torch.manual_seed(3)
+    m = GatedAttention(cfg, 0)
+    d = 256
+    m.q_proj = torch.nn.Linear(d, 4 * 2 * 64, bias=False)
+    m.k_proj = torch.nn.Linear(d, 2 * 64, bias=False)
+    m.v_proj = torch.nn.Linear(d, 2 * 64, bias=False)
+    m.o_proj = torch.nn.Linear(4 * 64, d, bias=False)
+    m = m.eval().to(DEV, dtype)
+    cos_t, sin_t = oracle.rope_tables(32, 64, 1e6)
+    for got, ref in _hip_against_cpu(m, d, (2, 64), cos_t, sin_t, 4, lambda T: "hip"):
         assert max_abs(got, ref) <= (1e-4 if dtype == torch.float32 else 2e-2)
