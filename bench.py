@@ -284,10 +284,22 @@ def cpu_baseline_decode(wl: DecodeWorkload, budget_s: float = 15.0) -> dict:
         total_b += 2 * K * wl.visible(L) * D * s + 2 * H * wl.T * D * s
         if total_t * (reps + 1) > budget_s:
             break
+    # the same rows in fp32 (same algorithmic bytes), one run each after a warm-up
+    t32 = 0.0
+    for b in range(rows):
+        L = wl.lens[b]
+        kc = layer[0][b:b + 1, :, :L].float().cpu()
+        vc = layer[1][b:b + 1, :, :L].float().cpu()
+        q32 = q[b:b + 1].float()
+        oracle.ragged_decode(q32, kc, vc, [L], wl.window, wl.scale)
+        t0 = time.perf_counter()
+        oracle.ragged_decode(q32, kc, vc, [L], wl.window, wl.scale)
+        t32 += time.perf_counter() - t0
     return {"value": round(total_b / total_t / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"rows 0..{rows - 1} of the C4 batch ({sum(wl.lens[:rows])} cached tokens), one layer, "
                       f"bf16 torch SDPA on the host CPU, median-free mean of 3 runs per row",
+            "value_fp32": round(total_b / t32 / 1e9, 3),
             "cpu": cpu_info()}
 
 
@@ -310,8 +322,17 @@ def cpu_baseline_prefill(B, T, H, K, D, budget_s: float = 10.0) -> dict:
         n += 1
     dt = (time.perf_counter() - t0) / n
     fl = 4.0 * D * H * T * (T + 1) / 2
+    q, k, v = q.float(), k.float(), v.float()  # the same in fp32
+    f()
+    t0 = time.perf_counter()
+    n32 = 0
+    while time.perf_counter() - t0 < budget_s / 4 or n32 < 2:
+        f()
+        n32 += 1
+    dt32 = (time.perf_counter() - t0) / n32
     return {"value": round(fl / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"1 of the {B} batch rows ({T} tokens causal), bf16 torch SDPA, mean of {n} runs"}
+            "sample": f"1 of the {B} batch rows ({T} tokens causal), bf16 torch SDPA, mean of {n} runs",
+            "value_fp32": round(fl / dt32 / 1e12, 4)}
 
 
 # ----------------------------------------------------------------------------- main
