@@ -748,13 +748,26 @@ void verify_mfma_kernel(SplitParams p) {
   float* tab = reinterpret_cast<float*>(smem + TL::STAGES * 2 * TL::TILEB);  // [gains | cos tok | sin tok][D]
 #pragma unroll
   for (int i = 0; i < TL::STAGES - 1; ++i) issue(i);
-  // q of this lane's row, loaded unconditionally (rows past the end read row 0 of head
-  // kvh * G and are zeroed below): a conditional load made the compiler wait for it here
-  uint4 qraw[KSTEPS];
+  // The q prologue is split over the waves: this lane normalises and rotates row
+  // qr = 8 * wave + lane / 8 of the unit, first-half channels qx .. qx + QCH - 1 and their
+  // RoPE partners qx + D/2. The q values are loaded unconditionally (rows past the end read
+  // row 0 of head kvh * G and are zeroed below): a conditional load made the compiler wait
+  // for it here.
+  constexpr int QCH = D / 16;  // first-half channels per lane, 8 lanes per row
+  const int qr = 8 * wave + (lane >> 3);
+  const int qx = QCH * (lane & 7);
+  const int qflat = rb * TL::ROWS + qr;
+  const bool qvalid = qflat < p.rows_total;
+  const int qtok = qvalid ? qflat / p.G : 0;
+  uint4 qa[QCH / 8], qz[QCH / 8];
   {
-    const T* src = static_cast<const T*>(p.q) + b * p.sqb + h * p.sqh + t * p.sqt;
+    const int qh = kvh * p.G + (qvalid ? qflat % p.G : 0);
+    const T* src = static_cast<const T*>(p.q) + b * p.sqb + qh * p.sqh + qtok * p.sqt + qx;
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) qraw[s] = load16(src + 16 * s + 8 * hi);
+    for (int j = 0; j < QCH / 8; ++j) {
+      qa[j] = load16(src + 8 * j);
+      qz[j] = load16(src + D / 2 + 8 * j);
+    }
   }
   {
     // every value's load goes out before the first store (one round trip, not one per value)
@@ -785,53 +798,56 @@ void verify_mfma_kernel(SplitParams p) {
   }
   __syncthreads();  // tables in LDS (the tile loads may still be in flight)
 
-  // Q^T operands of this lane's row: channels 16s + 8hi + e, fused RMSNorm + RoPE in fp32,
-  // one rounding (as the split kernel's q prologue; the RoPE partner of channel x is x+D/2).
-  V8 qreg[KSTEPS];
+  // Fused RMSNorm + RoPE of this lane's q values in fp32, one rounding (as the split
+  // kernel's q prologue), staged as T in the K slot of the last stage (not loaded until the
+  // loop's first barrier); then every wave reads the Q^T operands of its lane's row n:
+  // channels 16s + 8hi + e.
+  T* qs = reinterpret_cast<T*>(smem + (2 * (TL::STAGES - 1)) * TL::TILEB);  // [ROWS][D]
   {
-    if (!valid) {
+    float a[QCH], z[QCH];
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) qraw[s] = make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < QCH / 8; ++j) {
+      unpack16<T>(qa[j], a + 8 * j);
+      unpack16<T>(qz[j], z + 8 * j);
+    }
+    if (!qvalid) {
+#pragma unroll
+      for (int e = 0; e < QCH; ++e) a[e] = z[e] = 0.0f;
     }
     float rs = 1.0f;  // RMSNorm factor (1 without FORGE_NORM_QK)
     if (p.flags & FORGE_NORM_QK) {
       float ss = 0.0f;
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        float f[8];
-        unpack16<T>(qraw[s], f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
-      }
-      ss += __shfl_xor(ss, 32, kWave);
+      for (int e = 0; e < QCH; ++e) ss += a[e] * a[e] + z[e] * z[e];
+      ss += __shfl_xor(ss, 1, kWave);
+      ss += __shfl_xor(ss, 2, kWave);
+      ss += __shfl_xor(ss, 4, kWave);
       rs = rsqrtf(ss / (float)D + p.eps);
     }
-    const float* cr = tab + (1 + (t - tok_lo)) * D;
-    const float* sr = tab + (1 + TL::MAX_TOK + (t - tok_lo)) * D;
-    // channels x..x+7 (step s) and their RoPE partners x + D/2 (step s + KSTEPS/2)
 #pragma unroll
-    for (int s = 0; s < KSTEPS / 2; ++s) {
-      const int x = 16 * s + 8 * hi;
-      float a[8], z[8];
-      unpack16<T>(qraw[s], a);
-      unpack16<T>(qraw[s + KSTEPS / 2], z);
+    for (int j = 0; j < QCH / 8; ++j) {
+      const int x = qx + 8 * j;
+      float* aj = a + 8 * j;
+      float* zj = z + 8 * j;
       if (gains) {
         float wa[8], wz[8];
         load_f32x8(tab + x, wa);
         load_f32x8(tab + x + D / 2, wz);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          a[e] = a[e] * rs * wa[e];
-          z[e] = z[e] * rs * wz[e];
+          aj[e] = aj[e] * rs * wa[e];
+          zj[e] = zj[e] * rs * wz[e];
         }
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          a[e] *= rs;
-          z[e] *= rs;
+          aj[e] *= rs;
+          zj[e] *= rs;
         }
       }
-      if (rope && valid) {
+      if (rope && qvalid) {
+        const float* cr = tab + (1 + (qtok - tok_lo)) * D;
+        const float* sr = tab + (1 + TL::MAX_TOK + (qtok - tok_lo)) * D;
         float c1[8], s1[8], c2[8], s2[8];
         load_f32x8(cr + x, c1);
         load_f32x8(sr + x, s1);
@@ -839,18 +855,19 @@ void verify_mfma_kernel(SplitParams p) {
         load_f32x8(sr + x + D / 2, s2);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float a0 = a[e], z0 = z[e];
-          a[e] = a0 * c1[e] - z0 * s1[e];
-          z[e] = z0 * c2[e] + a0 * s2[e];
+          const float a0 = aj[e], z0 = zj[e];
+          aj[e] = a0 * c1[e] - z0 * s1[e];
+          zj[e] = z0 * c2[e] + a0 * s2[e];
         }
       }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        qreg[s][e] = from_f32<T>(a[e]);
-        qreg[s + KSTEPS / 2][e] = from_f32<T>(z[e]);
-      }
+      *reinterpret_cast<uint4*>(qs + qr * D + x) = pack16<T>(aj);
+      *reinterpret_cast<uint4*>(qs + qr * D + D / 2 + x) = pack16<T>(zj);
     }
   }
+  __syncthreads();  // the block's q rows are in LDS
+  V8 qreg[KSTEPS];
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s) qreg[s] = *reinterpret_cast<const V8*>(qs + n * D + 16 * s + 8 * hi);
 
   // LDS read offsets within a tile (as the prefill kernel's)
   const int k_rd = n * TL::ROWB;
