@@ -67,8 +67,10 @@ __global__ __launch_bounds__(256) void row_norm_rope_kernel(RowParams p) {
   const bool second = row >= rows0;
   const RowTensor& rt = second ? p.t[1] : p.t[0];
   const int64_t r = second ? row - rows0 : row;
-  const int t = (int)(r % p.T);
-  const int h = (int)((r / p.T) % rt.heads);
+  // heads fastest: the groups of a wave share one token's RoPE row (cache hits), and
+  // read neighbouring heads of the projection (C3 append 29.4 -> 28.7 us)
+  const int h = (int)(r % rt.heads);
+  const int t = (int)((r / rt.heads) % p.T);
   const int b = (int)(r / ((int64_t)p.T * rt.heads));
 
   const int half = p.D / 2;
