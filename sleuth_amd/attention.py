@@ -111,16 +111,17 @@ class Attention(nn.Module):
         if self._qkv_key != key():
             if any(m.weight.dtype != x.dtype or m.weight.device != x.device for m in mods):
                 return None
-            w = torch.cat([m.weight.detach() for m in mods], 0)
-            has_b = mods[0].bias is not None
-            b = torch.cat([m.bias.detach() for m in mods], 0) if has_b else None
-            off = 0
-            for m in mods:
-                n = m.weight.shape[0]
-                m.weight.data = w[off:off + n]
-                if has_b:
-                    m.bias.data = b[off:off + n]
-                off += n
+            with torch.inference_mode(False):  # ordinary tensors, also under inference_mode
+                w = torch.cat([m.weight.detach() for m in mods], 0)
+                has_b = mods[0].bias is not None
+                b = torch.cat([m.bias.detach() for m in mods], 0) if has_b else None
+                off = 0
+                for m in mods:
+                    n = m.weight.shape[0]
+                    m.weight.data = w[off:off + n]
+                    if has_b:
+                        m.bias.data = b[off:off + n]
+                    off += n
             self._qkv_w, self._qkv_b = w, b
             self._qkv_key = key()
         return F.linear(x, self._qkv_w, self._qkv_b)

@@ -311,6 +311,14 @@ def test_fused_qkv_projection_matches_separate():
         fused2 = a(x, cos, sin)
         assert max_abs(fused2.float().cpu(), separate().float().cpu()) <= 2e-2
         assert not torch.equal(fused2, fused)
+    # built under inference_mode, the buffer is an ordinary tensor: plain no_grad calls and
+    # in-place updates still work afterwards
+    b = Attention(cfg, 0).eval().to(DEV, torch.bfloat16)
+    with torch.inference_mode():
+        b(x, cos, sin)
+    with torch.no_grad():
+        b.q_proj.weight.mul_(1.5)
+        assert torch.isfinite(b(x, cos, sin)).all()
 
 
 def _hip_against_cpu(mod, d_model, kv, cos_t, sin_t, seed, expect_hip):
