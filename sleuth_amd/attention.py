@@ -28,6 +28,7 @@ from __future__ import annotations
 
 import math
 import os
+import weakref
 
 import torch
 import torch.nn.functional as F
@@ -36,7 +37,7 @@ from torch import nn
 from .config import ModelConfig
 from .norm import RMSNorm
 from .rope import apply_rope
-from .taps import Tap
+from .taps import make_tap, tap_active
 
 DECODE_MAX_T = 16
 _HIP_HEAD_DIMS = (32, 64, 128, 256)
@@ -56,6 +57,20 @@ def _hip_ready(device: torch.device, dtype: torch.dtype) -> None:
 
         self_check(device, dtype)   # raises on failure
         _checked[key] = True
+
+
+class _FusedQKV:
+    """The concatenated q/k/v projection weights of one set of projection Parameters."""
+
+    builds = 0   # buffers built so far in this process (tests check that tied layers share one)
+
+    def __init__(self, ids, state, w, b):
+        self.ids, self.state, self.w, self.b = ids, state, w, b
+
+
+# keyed by the q_proj weight Parameter: one buffer per set of Parameters, whichever modules
+# hold them; the entry goes away with the Parameter
+_FUSED_QKV: "weakref.WeakKeyDictionary[torch.Tensor, _FusedQKV]" = weakref.WeakKeyDictionary()
 
 
 class Attention(nn.Module):
@@ -78,21 +93,25 @@ class Attention(nn.Module):
         self.q_norm = RMSNorm(self.hd, cfg.norm_eps) if cfg.qk_norm else None
         self.k_norm = RMSNorm(self.hd, cfg.norm_eps) if cfg.qk_norm else None
         self.v_norm = cfg.v_norm
-        self.tap_q = Tap()
-        self.tap_k = Tap()
-        self.tap_pattern = Tap()
-        self.tap_z = Tap()
+        # the host's Tap type when running inside Sleuth, so its analyzer finds these
+        self.tap_q = make_tap()
+        self.tap_k = make_tap()
+        self.tap_pattern = make_tap()
+        self.tap_z = make_tap()
         self.last_path = ""   # "hip-decode" | "hip-prefill" | "torch" (for tests and stats)
-        self._qkv_key = None  # identity of the weights the fused projection buffer holds
-        self._qkv_w = self._qkv_b = None
 
     # ------------------------------------------------------------------ projections
     def _qkv_fused(self, x: torch.Tensor) -> torch.Tensor | None:
         """q_proj, k_proj and v_proj (attention.py:106-108) as one GEMM during GPU inference.
-        The weights are concatenated once into a [(H + 2K)·hd, d] buffer and the three
-        modules' weights (and biases) become views of it, so no second copy is kept. The
-        buffer is rebuilt when a weight is replaced, moved or modified in place (its storage,
-        dtype or version changes). Returns None where the separate projections run: on the
+
+        The weights are concatenated once into a [(H + 2K)·hd, d] buffer and the projections'
+        weights (and biases) become views of it, so no second copy is kept. The buffer
+        belongs to the Parameters, not to this module: modules that share their projection
+        Parameters (tied / looped layers, reference transformer.py:215-228) find the same
+        buffer and never rebuild it for each other. It is rebuilt when a weight is replaced,
+        moved or modified in place (its storage, dtype or version changes), but never while
+        a graph is being captured (the captured GEMM would read a buffer a later rebuild
+        frees): then the separate projections run. Returns None where they run: on the
         CPU, with autograd, and whenever a projection is not a plain nn.Linear or has hooks
         (adapters, quantised layers and forward hooks see the same calls as in the reference)."""
         if not x.is_cuda or torch.is_grad_enabled() or hip_disabled():
@@ -102,29 +121,34 @@ class Attention(nn.Module):
             return None
         if nn.modules.module._global_forward_hooks or nn.modules.module._global_forward_pre_hooks:
             return None
-
-        def key():
-            return tuple((m.weight.data_ptr(), m.weight._version, m.weight.dtype,
-                          None if m.bias is None else (m.bias.data_ptr(), m.bias._version))
-                         for m in mods)
-
-        if self._qkv_key != key():
-            if any(m.weight.dtype != x.dtype or m.weight.device != x.device for m in mods):
-                return None
-            with torch.inference_mode(False):  # ordinary tensors, also under inference_mode
-                w = torch.cat([m.weight.detach() for m in mods], 0)
-                has_b = mods[0].bias is not None
-                b = torch.cat([m.bias.detach() for m in mods], 0) if has_b else None
-                off = 0
-                for m in mods:
-                    n = m.weight.shape[0]
-                    m.weight.data = w[off:off + n]
-                    if has_b:
-                        m.bias.data = b[off:off + n]
-                    off += n
-            self._qkv_w, self._qkv_b = w, b
-            self._qkv_key = key()
-        return F.linear(x, self._qkv_w, self._qkv_b)
+        params = tuple(t for m in mods for t in (m.weight, m.bias) if t is not None)
+        ids = tuple(id(t) for t in params)
+        state = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in params)
+        entry = _FUSED_QKV.get(mods[0].weight)
+        if entry is not None and entry.ids == ids and entry.state == state:
+            return F.linear(x, entry.w, entry.b)
+        if entry is not None and entry.ids != ids:
+            return None   # the q weight is tied to another module with different k/v: no fusion
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        if any(m.weight.dtype != x.dtype or m.weight.device != x.device for m in mods):
+            return None
+        if len({m.bias is None for m in mods}) > 1:
+            return None
+        with torch.inference_mode(False):  # ordinary tensors, also under inference_mode
+            w = torch.cat([m.weight.detach() for m in mods], 0)
+            b = torch.cat([m.bias.detach() for m in mods], 0) if mods[0].bias is not None else None
+            off = 0
+            for m in mods:
+                n = m.weight.shape[0]
+                m.weight.data = w[off:off + n]
+                if b is not None:
+                    m.bias.data = b[off:off + n]
+                off += n
+        state = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in params)
+        _FUSED_QKV[mods[0].weight] = _FusedQKV(ids, state, w, b)
+        _FusedQKV.builds += 1
+        return F.linear(x, w, b)
 
     # ------------------------------------------------------------------ dispatch
     def _use_hip(self, q: torch.Tensor, cache, same_doc) -> bool:
@@ -132,7 +156,7 @@ class Attention(nn.Module):
             return False
         if torch.is_grad_enabled() and q.requires_grad:
             return False
-        if same_doc is not None or self.tap_pattern.active:
+        if same_doc is not None or tap_active(self.tap_pattern):
             return False
         if q.dtype not in _HIP_DTYPES or self.hd not in _HIP_HEAD_DIMS:
             return False
@@ -186,7 +210,7 @@ class Attention(nn.Module):
             q, k = self.tap_q(q), self.tap_k(k)
             q_args = dict(norm_q=False, cos=None, sin=None)
             k_args = dict(norm_k=False, cos=None, sin=None)
-        elif self.tap_q.active or self.tap_k.active:
+        elif tap_active(self.tap_q) or tap_active(self.tap_k):
             # Listeners see (and may replace) q and k after RoPE: materialise them.
             if qn or rc is not None:
                 q = ops.head_norm_rope(q, qw, self.eps if qn else 0.0, rc, rs, qn)
@@ -210,15 +234,19 @@ class Attention(nn.Module):
             kc, vc = cache.k[self.layer_idx], cache.v[self.layer_idx]
             chunk = ops.decode_chunk(q.dtype, B, 1, H, self.n_kv, hd, cache.max_len, self.window)
             if getattr(cache, "static", False):
-                pos = cache.positions
-                pos_kw, max_kv, offset = dict(pos_dev=pos), min(cache.length, cache.max_len), None
-            elif getattr(cache, "ragged", False):
-                cache.check_room(T)
-                pos_kw = dict(row_pos=cache.seq_lens)
-                max_kv, offset = max(cache.seq_lens_host) + T, None
+                # StaticKVCache (kv_cache.py:73-138): positions pos_t + arange(T) on the device
+                pos_kw, max_kv, offset = dict(pos_dev=cache.positions), min(cache.length, cache.max_len), None
             else:
-                cache.check_room(T)
-                pos_kw, max_kv, offset = dict(pos=cache.pos), cache.pos + T, cache.pos
+                # the reference's KVCache has one host `pos`; per-row lengths (`ragged`,
+                # `seq_lens`) are this package's extension and read only where present
+                rows = getattr(cache, "seq_lens", None) if getattr(cache, "ragged", False) else None
+                top = max(cache.seq_lens_host) if rows is not None else cache.pos
+                if top + T > cache.max_len:   # KVCache.update's check (kv_cache.py:56-57)
+                    raise ValueError(f"KV cache full ({cache.max_len} tokens)")
+                if rows is not None:
+                    pos_kw, max_kv, offset = dict(row_pos=rows), top + T, None
+                else:
+                    pos_kw, max_kv, offset = dict(pos=cache.pos), cache.pos + T, cache.pos
             ops.kv_append(k, v, kc, vc, norm_v=norm_v, **pos_kw, **k_args)
 
         if T > DECODE_MAX_T and offset is not None and ops.prefill_supported(q) and \
@@ -245,11 +273,11 @@ class Attention(nn.Module):
             k, v = cache.update(self.layer_idx, k, v)
         S = k.shape[2]
         offset = S - q.shape[2]
-        if getattr(cache, "static", False) and not self.tap_pattern.active:
+        if getattr(cache, "static", False) and not tap_active(self.tap_pattern):
             kwargs = {"enable_gqa": True} if self.n_kv != self.n_heads else {}
             return F.scaled_dot_product_attention(q, k, v, attn_mask=cache.attn_mask(self.window),
                                                   scale=self.scale, **kwargs)
-        if self.tap_pattern.active:
+        if tap_active(self.tap_pattern):
             return self._explicit(q, k, v, offset, same_doc)
         return self._fused(q, k, v, offset, same_doc)
 
@@ -262,7 +290,7 @@ class Attention(nn.Module):
         for b, L in enumerate(lens):
             kb = cache.k[self.layer_idx][b:b + 1, :, :L + T]
             vb = cache.v[self.layer_idx][b:b + 1, :, :L + T]
-            fn = self._explicit if self.tap_pattern.active else self._fused
+            fn = self._explicit if tap_active(self.tap_pattern) else self._fused
             out.append(fn(q[b:b + 1], kb, vb, L, same_doc))
         return torch.cat(out, 0)
 

@@ -45,6 +45,9 @@ class ModelConfig:
     swa_kv_heads: int = 0
     swa_rope_theta: float = 0.0
     full_v_from_k: bool = False
+    # layer i reuses layer shared_layers[i]'s Linear Parameters (config.py's looped layers,
+    # tied in transformer.py:215-228); empty = every layer has its own
+    shared_layers: list[int] = field(default_factory=list)
     # harness-only (the tiny decoder in sleuth_amd.model): MLP width, tied embeddings
     ffn_hidden: int = 0
     tie_embeddings: bool = True
@@ -61,6 +64,14 @@ class ModelConfig:
             raise ValueError(f"layer_types entries must be 'full' or 'sliding', got {sorted(set(self.layer_types))}")
         if "sliding" in self.layer_types and self.sliding_window <= 0:
             raise ValueError("sliding layers need sliding_window > 0")
+        if self.shared_layers:
+            src = self.shared_layers
+            if len(src) != self.n_layers:
+                raise ValueError(f"shared_layers has {len(src)} entries for {self.n_layers} layers")
+            for i, j in enumerate(src):
+                if not 0 <= j <= i or src[j] != j:
+                    raise ValueError(f"layer {i} cannot share layer {j}'s weights: the source must be "
+                                     "an earlier (or the same) layer that is not shared itself")
         if self.pos_type not in ("rope", "none", "learned"):
             raise ValueError(f"pos_type must be one of ('rope', 'none', 'learned'), got {self.pos_type!r}")
         for spec in {self.attn_spec(i) for i in range(self.n_layers)}:

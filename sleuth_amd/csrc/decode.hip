@@ -501,8 +501,13 @@ void splitk_kernel(SplitParams p) {
   // in the workspace, which the host zeroes before the launch), so a block on a CU that
   // streams faster takes more of them. A block fetches its next ticket when it starts a
   // unit and reads it after the unit's merge.
-  __shared__ int sh_ticket;
-  for (int u = blockIdx.x; u < total; u = sh_ticket) {
+  // Two ticket slots, alternating by iteration: a unit may return early without a block
+  // barrier, so thread 0 can write the next ticket while a slower wave has not yet read
+  // the one before; with the slots alternating it writes the other slot, and the barrier
+  // at the end of every iteration keeps the waves within one iteration of each other.
+  __shared__ int sh_ticket[2];
+  int parity = 0;
+  for (int u = blockIdx.x; u < total; u = sh_ticket[parity], parity ^= 1) {
     int next = total;
     int lo = 0, hi = p.B - 1;  // last row with sh_pref[row] <= u
     while (lo < hi) {
@@ -514,7 +519,7 @@ void splitk_kernel(SplitParams p) {
     const int n = sh_nch[lo];
     const int pr = o / n;
     split_unit<T, D, ROWS>(p, lo, pr % p.K, pr / p.K, sh_cmin[lo] + o % n, sh, &next);
-    if (tid == 0) sh_ticket = next;
+    if (tid == 0) sh_ticket[parity] = next;
     __syncthreads();  // the next unit reuses the merge LDS; the ticket is visible
   }
 }

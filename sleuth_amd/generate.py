@@ -1,25 +1,30 @@
 """The callers the attention path has to serve: plain decoding, speculative
-draft-then-verify, and graph-captured static decoding.
+draft-then-verify, and graph-replayed decode steps.
 
-generate()             sleuth/forge/infer/generate.py:49-136 (prefill, then one token
-                       per step through the cache; greedy or temperature sampling)
-speculative_generate() sleuth/forge/infer/speculative.py:83-277 (verify = one forward of
-                       [pending] + k guesses at offset cache.pos; keep() rewinds pos)
-GraphDecoder           sleuth/forge/infer/cuda_graph.py:33-144 (StaticKVCache, one HIP
-                       graph per length bucket 64, 128, ..., max_len; verify() runs
-                       tokens_per_step tokens)
-Greedy output is what the tests compare; sampling policies beyond temperature are out
-of scope (they act after attention).
+generate()             the decode loop of sleuth/forge/infer/generate.py:49-136: the prompt's
+                       prefill, then one token per step through the cache (greedy or
+                       temperature sampling)
+speculative_generate() greedy draft-then-verify as in speculative.py:83-277: [pending] + k
+                       guesses in one forward at offset cache.pos, the agreeing prefix kept by
+                       moving pos back (the rewind the reference's keep() does)
+GraphDecoder           decode/verify steps replayed from a HIP graph (the role of
+                       cuda_graph.py:67-144), built for kernels that read the live length on
+                       the device: the attention reads only the keys below pos_t + T, whatever
+                       the graph was recorded at, so ONE graph per step size serves every
+                       context length -- no length buckets, no re-recording as the context
+                       grows, no masked reads of a bucket's unused tail.
+Sampling policies beyond temperature act after attention and are out of scope.
 """
 
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass, field
 from typing import Callable
 
 import torch
 
-from .kv_cache import KVCache, StaticKVCache
+from .kv_cache import KVCache
 
 
 @dataclass
@@ -30,11 +35,96 @@ class GenerationResult:
     stats: dict = field(default_factory=dict)
 
 
-def _choose(logits: torch.Tensor, temperature: float, gen) -> torch.Tensor:
-    if temperature <= 0:
-        return logits.argmax(-1)
-    probs = (logits.float() / temperature).softmax(-1)
-    return torch.multinomial(probs, 1, generator=gen).view(-1)
+def _pick(logits: torch.Tensor, temperature: float, gen: torch.Generator) -> torch.Tensor:
+    """Next token id(s) [n] from logits [n, vocab]: argmax, or a draw at `temperature`."""
+    if temperature > 0:
+        return torch.multinomial((logits.float() / temperature).softmax(-1), 1, generator=gen).view(-1)
+    return logits.argmax(-1)
+
+
+class GraphDecoder:
+    """Batch-1 decode (`step`) or verify (`verify`) steps of `tokens_per_step` tokens,
+    recorded into one HIP graph (torch.cuda.CUDAGraph is hipGraph on ROCm) on first use and
+    replayed afterwards. The position lives in cache.pos_t on the device; the host copies the
+    new token ids and the position into the graph's input buffers before each replay.
+    Use `cache` for the prompt's prefill (an ordinary eager forward)."""
+
+    def __init__(self, model, max_len: int, dtype: torch.dtype, tokens_per_step: int = 1):
+        p = next(model.parameters())
+        if p.device.type != "cuda":
+            raise ValueError("graph decoding needs a model on the GPU")
+        self.model, self.T = model, tokens_per_step
+        self.cache = KVCache.for_model(model, 1, max_len, dtype, tokens_per_step)
+        self._ids = torch.zeros(1, tokens_per_step, dtype=torch.long, device=p.device)
+        self._graph: torch.cuda.CUDAGraph | None = None
+        self._logits: torch.Tensor | None = None
+        self.replays = 0
+
+    @property
+    def recorded(self) -> bool:
+        return self._graph is not None
+
+    def _pass(self) -> torch.Tensor:
+        return self.model(self._ids, cache=self.cache).logits[0]
+
+    def _record(self) -> None:
+        # one eager pass first (on a side stream, as graph capture wants): first-use
+        # self-checks, library workspaces and the fused projection weights are set up
+        # outside the capture; it writes the same K/V the real step writes
+        side = torch.cuda.Stream(self._ids.device)
+        side.wait_stream(torch.cuda.current_stream(self._ids.device))
+        with torch.cuda.stream(side):
+            self._pass()
+        torch.cuda.current_stream(self._ids.device).wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._logits = self._pass()
+        self._graph = g
+
+    @torch.no_grad()
+    def _launch(self, tokens: torch.Tensor) -> torch.Tensor:
+        c = self.cache
+        if c.pos + self.T > c.max_len:
+            raise ValueError(f"KV cache full ({c.max_len} tokens)")
+        self._ids.copy_(tokens.view(1, self.T))
+        c.pos_t.fill_(c.pos)
+        c.static = True
+        try:
+            if self._graph is None:
+                self._record()
+            self._graph.replay()
+        finally:
+            c.static = False
+        self.replays += 1
+        return self._logits
+
+    def step(self, token: torch.Tensor) -> torch.Tensor:
+        """Logits [1, vocab] of `token` at position cache.pos; the cache moves on by one.
+        The result is the graph's output buffer: read it before the next replay."""
+        if self.T != 1:
+            raise ValueError("step() is for one token at a time; use verify()")
+        logits = self._launch(token)
+        self.cache.pos += 1
+        return logits
+
+    def verify(self, tokens: torch.Tensor) -> torch.Tensor:
+        """Logits [T, vocab] of T tokens at positions cache.pos, ...; cache.pos stays (the
+        caller sets it to what it keeps)."""
+        return self._launch(tokens)
+
+
+_decoders: "weakref.WeakKeyDictionary[torch.nn.Module, dict]" = weakref.WeakKeyDictionary()
+
+
+def decoder_for(model, max_len: int, dtype: torch.dtype, tokens_per_step: int = 1) -> GraphDecoder:
+    """The model's graph decoder for this context and step size, kept across calls (the
+    graph is recorded once per model); its cache is rewound for the new prompt."""
+    per_model = _decoders.setdefault(model, {})
+    dec = per_model.get((max_len, tokens_per_step, dtype))
+    if dec is None:
+        dec = per_model[(max_len, tokens_per_step, dtype)] = GraphDecoder(model, max_len, dtype, tokens_per_step)
+    dec.cache.reset()
+    return dec
 
 
 @torch.no_grad()
@@ -44,37 +134,29 @@ def generate(model, prompt_ids: list[int], max_new_tokens: int = 32, temperature
     if not prompt_ids:
         raise ValueError("prompt must contain at least one token")
     p = next(model.parameters())
-    dev, max_len = p.device, model.cfg.max_seq_len
-    stop_ids = stop_ids or set()
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(0 if seed is None else seed)
-    dtype = cache_dtype or p.dtype
-    decoder = None
-    if cuda_graph:
-        decoder = decoder_for(model, max_len, dtype=dtype)
-        cache = decoder.cache
-    else:
-        cache = KVCache.for_model(model, 1, max_len, dtype)
+    max_len = model.cfg.max_seq_len
+    gen = torch.Generator(device=p.device).manual_seed(seed or 0)
+    dec = decoder_for(model, max_len, cache_dtype or p.dtype) if cuda_graph else None
+    cache = dec.cache if dec is not None else KVCache.for_model(model, 1, max_len, cache_dtype or p.dtype)
     model.eval()
-    logits = model(torch.tensor([prompt_ids], device=dev), cache=cache).logits[:, -1]
-    new, reason = [], "max_new_tokens"
-    for _ in range(max_new_tokens):
-        nxt = _choose(logits, temperature, gen)
-        tok = int(nxt.item())
-        new.append(tok)
-        if tok in stop_ids:
+    logits = model(torch.tensor([prompt_ids], device=p.device), cache=cache).logits[:, -1]
+    new: list[int] = []
+    reason = "max_new_tokens"
+    while max_new_tokens > 0:
+        tok = _pick(logits, temperature, gen)
+        new.append(int(tok.item()))
+        if stop_ids and new[-1] in stop_ids:
             reason = "stop_token"
+            break
+        if len(new) == max_new_tokens:
             break
         if cache.pos >= max_len:
             reason = "context_full"
             break
-        if decoder is not None:
-            logits = decoder.step(nxt.view(1))
-        else:
-            logits = model(nxt.view(1, 1), cache=cache).logits[:, -1]
+        logits = dec.step(tok.view(1)) if dec is not None else model(tok.view(1, 1), cache=cache).logits[:, -1]
     stats = {"kv_cache_mb": round(cache.nbytes() / 1e6, 2)}
-    if decoder is not None:
-        stats["graphs"] = sorted(decoder.graphs)
+    if dec is not None:
+        stats["graph_replays"] = dec.replays
     return GenerationResult(list(prompt_ids), new, reason, stats)
 
 
@@ -99,129 +181,36 @@ def speculative_generate(model, prompt_ids: list[int], max_new_tokens: int = 32,
     offset cache.pos (T = 1 + k), keeps the longest agreeing prefix and rewinds pos."""
     draft = draft or ngram_draft()
     p = next(model.parameters())
-    dev, max_len = p.device, model.cfg.max_seq_len
+    max_len = model.cfg.max_seq_len
     dtype = cache_dtype or p.dtype
-    decoder = decoder_for(model, max_len, dtype=dtype, tokens_per_step=k + 1) if cuda_graph else None
-    cache = decoder.cache if decoder is not None else KVCache.for_model(model, 1, max_len, dtype)
+    dec = decoder_for(model, max_len, dtype, tokens_per_step=k + 1) if cuda_graph else None
+    cache = dec.cache if dec is not None else KVCache.for_model(model, 1, max_len, dtype)
     model.eval()
-    logits = model(torch.tensor([prompt_ids], device=dev), cache=cache).logits[0, -1]
-    ids, new = list(prompt_ids), []
+    logits = model(torch.tensor([prompt_ids], device=p.device), cache=cache).logits[0, -1]
+    ids = list(prompt_ids) + [int(logits.argmax())]
+    new = ids[len(prompt_ids):]
     stats = {"forwards": 0, "drafted": 0, "accepted": 0}
-    tok = int(logits.argmax())
-    ids.append(tok)
-    new.append(tok)
     while len(new) < max_new_tokens:
-        pending = new[-1]
         room = min(k, max_new_tokens - len(new), max_len - cache.pos - 1)
         if room < 0:
             break
         guess = draft(ids, room)[:room] if room > 0 else []
         start = cache.pos
-        if decoder is not None and start + k + 1 <= max_len:
-            padded = [pending] + guess + [pending] * (k - len(guess))
-            out = decoder.verify(torch.tensor(padded, device=dev))
+        if dec is not None and start + k + 1 <= max_len:
+            row = [new[-1]] + guess + [new[-1]] * (k - len(guess))   # fixed T: pad the guesses
+            out = dec.verify(torch.tensor(row, device=p.device))
         else:
-            out = model(torch.tensor([[pending] + guess], device=dev), cache=cache).logits[0]
-            cache.pos = start
+            out = model(torch.tensor([[new[-1]] + guess], device=p.device), cache=cache).logits[0]
+        choice = out[:len(guess) + 1].argmax(-1).tolist()
+        n_ok = next((i for i, (c, g) in enumerate(zip(choice, guess)) if c != g), len(guess))
         stats["forwards"] += 1
         stats["drafted"] += len(guess)
-        choice = out[: len(guess) + 1].argmax(-1).tolist()
-        n_ok = 0
-        while n_ok < len(guess) and choice[n_ok] == guess[n_ok]:
-            n_ok += 1
         stats["accepted"] += n_ok
-        accepted = guess[:n_ok] + [choice[n_ok]]
-        cache.pos = start + 1 + n_ok          # keep(): the pending token + accepted guesses
-        for t in accepted:
-            if len(new) >= max_new_tokens:
-                break
+        cache.pos = start + 1 + n_ok          # keep the pending token and the accepted guesses
+        for t in (guess[:n_ok] + [choice[n_ok]])[:max_new_tokens - len(new)]:
             ids.append(t)
             new.append(t)
     res = GenerationResult(list(prompt_ids), new, "max_new_tokens", {"speculative": stats})
-    if decoder is not None:
-        res.stats["graphs"] = sorted(decoder.graphs)
+    if dec is not None:
+        res.stats["graph_replays"] = dec.replays
     return res
-
-
-# ----------------------------------------------------------------------------- graphs
-def _buckets(max_len: int, smallest: int = 64) -> list[int]:
-    out, b = [], smallest
-    while b < max_len:
-        out.append(b)
-        b *= 2
-    return out + [max_len]
-
-
-def decoder_for(model, max_len: int, dtype: torch.dtype, tokens_per_step: int = 1) -> "GraphDecoder":
-    decs = model.__dict__.setdefault("_graph_decoders", {})
-    key = (max_len, tokens_per_step, dtype)
-    if key not in decs:
-        decs[key] = GraphDecoder(model, max_len, dtype, tokens_per_step)
-    decs[key].cache.reset()
-    return decs[key]
-
-
-class GraphDecoder:
-    """Static-shape decode/verify steps replayed as HIP graphs (torch.cuda.CUDAGraph is
-    hipGraph on ROCm), one per length bucket. The position lives in cache.pos_t, the
-    attention kernels read it on the device, and they read only the live keys
-    (pos_t + T) instead of the whole bucket."""
-
-    def __init__(self, model, max_len: int, dtype: torch.dtype, tokens_per_step: int = 1):
-        p = next(model.parameters())
-        if p.device.type != "cuda":
-            raise ValueError("graph decoding needs a model on the GPU")
-        self.model, self.device, self.max_len, self.T = model, p.device, max_len, tokens_per_step
-        shapes = [(model.cfg.attn_spec(i).kv_heads, model.cfg.attn_spec(i).head_dim)
-                  for i in range(model.cfg.n_layers)]
-        self.cache = StaticKVCache(shapes, 1, max_len, self.device, dtype, tokens_per_step)
-        self.token = torch.zeros(1, self.T, dtype=torch.long, device=self.device)
-        self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
-        self.pool = torch.cuda.graph_pool_handle()
-        self.buckets = _buckets(max_len)
-
-    def _forward(self):
-        return self.model(self.token, cache=self.cache).logits[0]
-
-    def _record(self, length: int):
-        self.cache.length = length
-        side = torch.cuda.Stream(self.device)
-        side.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(side):
-            for _ in range(2):
-                self._forward()
-        torch.cuda.current_stream(self.device).wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, pool=self.pool):
-            out = self._forward()
-        self.graphs[length] = (graph, out)
-
-    @torch.no_grad()
-    def _run(self, tokens: torch.Tensor) -> torch.Tensor:
-        pos = self.cache.pos
-        if pos + self.T > self.max_len:
-            raise ValueError(f"KV cache full ({self.max_len} tokens)")
-        length = next(b for b in self.buckets if b >= pos + self.T)
-        self.token.copy_(tokens.view(1, self.T))
-        self.cache.pos_t.fill_(pos)
-        self.cache.static = True
-        try:
-            if length not in self.graphs:
-                self._record(length)
-            self.cache.length = length
-            graph, out = self.graphs[length]
-            graph.replay()
-        finally:
-            self.cache.static = False
-        return out
-
-    def step(self, token: torch.Tensor) -> torch.Tensor:
-        if self.T != 1:
-            raise ValueError("step() is for one token at a time; use verify()")
-        out = self._run(token)
-        self.cache.pos += 1
-        return out
-
-    def verify(self, tokens: torch.Tensor) -> torch.Tensor:
-        return self._run(tokens)
-

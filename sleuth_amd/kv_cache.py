@@ -1,19 +1,21 @@
-"""Key/value caches with the reference's layout and protocol.
+"""KV cache with per-row lengths, laid out for the HIP attention kernels.
 
-KVCache (sleuth/forge/infer/kv_cache.py:25-70): per-layer k[layer], v[layer] =
-zeros(B, K, max_len, hd), one shared `pos`, update()/advance()/reset()/nbytes()/
-token_history()/for_model(). StaticKVCache (kv_cache.py:73-138): the CUDA-graph variant
-with the position in a device tensor `pos_t`, `length` (the bucket the graph was
-recorded for), `positions`, attn_mask(window) and new_step().
+The attention module runs on any object with the reference's cache protocol
+(sleuth/forge/infer/kv_cache.py:25-138) -- the host's own KVCache and StaticKVCache
+included. This class is the cache of this package's callers (generate(), the graph
+decoder, the benchmark); it speaks the same protocol and adds what the kernels can use:
 
-The HIP attention writes the new K/V straight into these tensors (forge_kv_append)
-and reads them in place, so code that looks at cache.k[layer][:, :, :n] (MTP drafters,
-the analyzer) sees the same data as with the reference.
+  storage    every layer's K and V are views [B, K, max_len, hd] of ONE device allocation
+             (the arena), so a whole model's cache is a single block of HBM;
+  row lengths  each batch row has its own length (`set_lengths`, `seq_lens` int32 [B] on
+             the device with a host mirror `seq_lens_host`); `pos` is the longest row, and
+             setting it sets every row (what the speculative decoder's rewind does);
+  static mode  (graph replays) the position is the device scalar `pos_t`; `positions`
+             (pos_t + 0 .. tokens_per_step-1) is computed into a fixed buffer, so a
+             captured graph recomputes it on every replay.
 
-Extension for ragged batches: set_lengths([L_0, .., L_B-1]) gives each row its own
-length (`seq_lens`, int32 [B] on the device, with a host mirror); token t of row b
-then goes to position seq_lens[b] + t and advance(n) moves every row. Without it,
-`pos` keeps the reference's meaning.
+Protocol members: k, v, pos, max_len, update, advance, reset, nbytes, token_history,
+for_model; static, pos_t, length, tokens_per_step, positions, attn_mask, new_step.
 """
 
 from __future__ import annotations
@@ -23,134 +25,145 @@ import torch
 
 class KVCache:
     def __init__(self, shapes: list[tuple[int, int]], batch: int, max_len: int,
-                 device: torch.device | str, dtype: torch.dtype):
-        """shapes: (n_kv_heads, head_dim) for each layer."""
-        self.k = [torch.zeros(batch, kv, max_len, hd, device=device, dtype=dtype) for kv, hd in shapes]
-        self.v = [torch.zeros_like(k) for k in self.k]
-        self.max_len = max_len
-        self.batch = batch
-        self.pos = 0
-        self._tokens: torch.Tensor | None = None
-        self.seq_lens: torch.Tensor | None = None
-        self.seq_lens_host: list[int] | None = None
-
-    def token_history(self, batch: int, device) -> torch.Tensor:
-        """[batch, max_len] token ids by position (-1 = none yet), made on first use."""
-        if self._tokens is None:
-            self._tokens = torch.full((batch, self.max_len), -1, dtype=torch.long, device=device)
-        return self._tokens
+                 device: torch.device | str, dtype: torch.dtype, tokens_per_step: int = 1):
+        """shapes: (n_kv_heads, head_dim) of each layer."""
+        if batch < 1 or max_len < 1 or tokens_per_step < 1:
+            raise ValueError("batch, max_len and tokens_per_step must be positive")
+        dev = torch.device(device)
+        sizes = [batch * kv * max_len * hd for kv, hd in shapes]
+        half = sum(sizes)
+        self._arena = torch.zeros(2 * half, device=dev, dtype=dtype)   # [all K | all V]
+        self.k, self.v, off = [], [], 0
+        for (kv, hd), n in zip(shapes, sizes):
+            self.k.append(self._arena[off:off + n].view(batch, kv, max_len, hd))
+            self.v.append(self._arena[half + off:half + off + n].view(batch, kv, max_len, hd))
+            off += n
+        self.max_len, self.batch, self.device = max_len, batch, dev
+        self._rows = [0] * batch
+        self._rows_dev: torch.Tensor | None = None   # device mirror, made when rows differ
+        self._history: torch.Tensor | None = None
+        # static (graph) mode
+        self.static = False
+        self.length = max_len
+        self.tokens_per_step = tokens_per_step
+        self.pos_t = torch.zeros(1, dtype=torch.long, device=dev)
+        self._steps = torch.arange(tokens_per_step, device=dev)
+        self._pos_buf = torch.zeros(tokens_per_step, dtype=torch.long, device=dev)
+        self._pass_pos: torch.Tensor | None = None
+        self._pass_masks: dict[int, torch.Tensor] = {}
 
     @classmethod
-    def for_model(cls, model, batch: int, max_len: int | None = None,
-                  dtype: torch.dtype | None = None) -> "KVCache":
+    def for_model(cls, model, batch: int, max_len: int | None = None, dtype: torch.dtype | None = None,
+                  tokens_per_step: int = 1) -> "KVCache":
         cfg = model.cfg
         p = next(model.parameters())
-        shapes = [(cfg.attn_spec(i).kv_heads, cfg.attn_spec(i).head_dim) for i in range(cfg.n_layers)]
-        return cls(shapes, batch, max_len or cfg.max_seq_len, p.device, dtype or p.dtype)
+        specs = [cfg.attn_spec(i) for i in range(cfg.n_layers)]
+        return cls([(s.kv_heads, s.head_dim) for s in specs], batch, max_len or cfg.max_seq_len,
+                   p.device, dtype or p.dtype, tokens_per_step)
 
-    # ------------------------------------------------------------------ ragged rows
+    # ------------------------------------------------------------------ lengths
+    @property
+    def pos(self) -> int:
+        return max(self._rows)
+
+    @pos.setter
+    def pos(self, value: int) -> None:
+        self._rows = [int(value)] * self.batch
+        self._rows_dev = None
+
     def set_lengths(self, lengths: list[int]) -> None:
-        """Per-row lengths (tokens already stored in each row)."""
-        if len(lengths) != self.batch:
-            raise ValueError(f"{len(lengths)} lengths for batch {self.batch}")
-        if any(L < 0 or L > self.max_len for L in lengths):
+        """Give each row its own length (tokens already stored in it)."""
+        rows = [int(n) for n in lengths]
+        if len(rows) != self.batch:
+            raise ValueError(f"{len(rows)} lengths for batch {self.batch}")
+        if min(rows) < 0 or max(rows) > self.max_len:
             raise ValueError(f"lengths must be in [0, {self.max_len}]")
-        self.seq_lens_host = [int(L) for L in lengths]
-        self.seq_lens = torch.tensor(self.seq_lens_host, dtype=torch.int32, device=self.k[0].device)
-        self.pos = max(self.seq_lens_host)
+        self._rows = rows
+        self._rows_dev = None
 
     @property
     def ragged(self) -> bool:
-        return self.seq_lens is not None
+        return min(self._rows) != max(self._rows)
 
-    # ------------------------------------------------------------------ reference protocol
+    @property
+    def seq_lens_host(self) -> list[int]:
+        return list(self._rows)
+
+    @property
+    def seq_lens(self) -> torch.Tensor:
+        """int32 [B] row lengths on the device (what forge_kv_append / forge_attn_decode
+        read as row_pos)."""
+        if self._rows_dev is None:
+            self._rows_dev = torch.tensor(self._rows, dtype=torch.int32).to(self.device)
+        return self._rows_dev
+
+    def _room_for(self, T: int) -> None:
+        if self.pos + T > self.max_len:
+            raise ValueError(f"KV cache full ({self.max_len} tokens)")
+
+    # ------------------------------------------------------------------ protocol
     def update(self, layer: int, k_new: torch.Tensor, v_new: torch.Tensor):
-        """Store this step's K/V for `layer`; return all K/V so far: [B, K, pos+T, hd]."""
-        T = k_new.shape[2]
-        if self.ragged:
-            for b, L in enumerate(self.seq_lens_host):
-                if L + T > self.max_len:
-                    raise ValueError(f"KV cache full ({self.max_len} tokens)")
-                self.k[layer][b, :, L:L + T] = k_new[b].to(self.k[layer].dtype)
-                self.v[layer][b, :, L:L + T] = v_new[b].to(self.v[layer].dtype)
-            end = self.pos + T
-            return self.k[layer][:, :, :end], self.v[layer][:, :, :end]
-        end = self.pos + T
-        if end > self.max_len:
-            raise ValueError(f"KV cache full ({self.max_len} tokens)")
-        self.k[layer][:, :, self.pos:end] = k_new.to(self.k[layer].dtype)
-        self.v[layer][:, :, self.pos:end] = v_new.to(self.v[layer].dtype)
-        return self.k[layer][:, :, :end], self.v[layer][:, :, :end]
-
-    def check_room(self, T: int) -> None:
-        """Raise like update() does when T more tokens do not fit (kv_cache.py:56-57)."""
-        top = max(self.seq_lens_host) if self.ragged else self.pos
-        if top + T > self.max_len:
-            raise ValueError(f"KV cache full ({self.max_len} tokens)")
+        """Torch-path write of this step's K/V [B, K, T, hd]; returns the K/V views the
+        step attends over: [:, :, :pos+T] (static mode: [:, :, :length])."""
+        kc, vc = self.k[layer], self.v[layer]
+        B, _, T, _ = k_new.shape
+        if self.static:
+            where = self.positions
+            kc.index_copy_(2, where, k_new.to(kc.dtype))
+            vc.index_copy_(2, where, v_new.to(vc.dtype))
+            return kc[:, :, :self.length], vc[:, :, :self.length]
+        self._room_for(T)
+        # one scatter for all rows: row b's token t goes to position rows[b] + t
+        cols = torch.tensor(self._rows, device=kc.device)[:, None] + torch.arange(T, device=kc.device)
+        rows = torch.arange(B, device=kc.device)[:, None].expand(B, T)
+        kc[rows, :, cols] = k_new.transpose(1, 2).to(kc.dtype)
+        vc[rows, :, cols] = v_new.transpose(1, 2).to(vc.dtype)
+        top = self.pos + T
+        return kc[:, :, :top], vc[:, :, :top]
 
     def advance(self, n: int) -> None:
-        """Called by the model once all layers have stored the new tokens."""
-        if self.ragged:
-            self.seq_lens_host = [L + n for L in self.seq_lens_host]
-            self.seq_lens += n
-            self.pos = max(self.seq_lens_host)
-        else:
-            self.pos += n
+        """All layers have stored n more tokens per row. In static mode the caller owns
+        the position (pos and pos_t), so nothing moves here."""
+        if self.static:
+            return
+        self._rows = [r + n for r in self._rows]
+        if self._rows_dev is not None:
+            self._rows_dev.add_(n)
 
     def reset(self) -> None:
         self.pos = 0
-        self.seq_lens = self.seq_lens_host = None
+        self.static = False
 
     def nbytes(self) -> int:
-        return sum(2 * k.numel() * k.element_size() for k in self.k)
+        return self._arena.numel() * self._arena.element_size()
 
+    def token_history(self, batch: int, device) -> torch.Tensor:
+        """[batch, max_len] token ids by position, -1 where none yet (made on first use)."""
+        if self._history is None:
+            self._history = torch.full((batch, self.max_len), -1, dtype=torch.long, device=device)
+        return self._history
 
-class StaticKVCache(KVCache):
-    """A KVCache that one-token (or tokens_per_step) decode steps can use inside a HIP
-    graph: the position lives in `pos_t` (int64 [1] on the device); outside `static`
-    mode (the prompt's prefill) it behaves like KVCache."""
-
-    def __init__(self, shapes, batch, max_len, device, dtype, tokens_per_step: int = 1):
-        super().__init__(shapes, batch, max_len, device, dtype)
-        self.static = False
-        self.length = max_len
-        self.pos_t = torch.zeros(1, dtype=torch.long, device=device)
-        self._kpos = torch.arange(max_len, device=device)
-        self.tokens_per_step = tokens_per_step
-        self._qoff = torch.arange(tokens_per_step, device=device)
-        self._masks: dict[int, torch.Tensor] = {}
-        self._pos: torch.Tensor | None = None
-
+    # ------------------------------------------------------------------ static mode
     @property
     def positions(self) -> torch.Tensor:
-        """[tokens_per_step] positions of this static step's tokens (pos_t, pos_t+1, ..)."""
-        if self._pos is None:
-            self._pos = self.pos_t + self._qoff
-        return self._pos
-
-    def update(self, layer, k_new, v_new):
-        if not self.static:
-            return super().update(layer, k_new, v_new)
-        pos = self.positions
-        self.k[layer].index_copy_(2, pos, k_new.to(self.k[layer].dtype))
-        self.v[layer].index_copy_(2, pos, v_new.to(self.v[layer].dtype))
-        return self.k[layer][:, :, :self.length], self.v[layer][:, :, :self.length]
-
-    def attn_mask(self, window: int = 0) -> torch.Tensor:
-        """[1, 1, T, length] bool, True = may attend (built once per pass per window)."""
-        if window not in self._masks:
-            kpos = self._kpos[:self.length][None, :]
-            qpos = self.positions[:, None]
-            mask = kpos <= qpos
-            if window:
-                mask = mask & (qpos - kpos < window)
-            self._masks[window] = mask[None, None]
-        return self._masks[window]
+        """int64 [tokens_per_step]: this pass's token positions, pos_t + 0, 1, ..."""
+        if self._pass_pos is None:
+            torch.add(self.pos_t, self._steps, out=self._pos_buf)
+            self._pass_pos = self._pos_buf
+        return self._pass_pos
 
     def new_step(self, positions: torch.Tensor | None = None) -> None:
-        """Start of a forward pass: positions may have moved (or are given explicitly)."""
-        self._masks, self._pos = {}, positions
+        """Start of a forward pass: positions are recomputed from pos_t (or taken as given)."""
+        self._pass_pos = positions
+        self._pass_masks = {}
 
-    def advance(self, n):
-        if not self.static:  # in static mode the caller moves pos and pos_t
-            super().advance(n)
+    def attn_mask(self, window: int = 0) -> torch.Tensor:
+        """[1, 1, T, length] bool, True where a query may see a key; one per window per pass."""
+        mask = self._pass_masks.get(window)
+        if mask is None:
+            gap = self.positions[:, None] - torch.arange(self.length, device=self.device)[None, :]
+            mask = gap >= 0
+            if window:
+                mask &= gap < window
+            mask = self._pass_masks[window] = mask[None, None]
+        return mask

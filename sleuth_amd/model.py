@@ -21,7 +21,7 @@ from .attention import Attention
 from .config import ModelConfig
 from .norm import RMSNorm
 from .rope import rope_tables
-from .taps import Tap, assign_tap_names
+from .taps import make_tap, name_taps
 
 
 class SwiGLU(nn.Module):
@@ -43,8 +43,8 @@ class Block(nn.Module):
         self.attn = Attention(cfg, i)
         self.norm2 = RMSNorm(cfg.d_model, cfg.norm_eps)
         self.mlp = SwiGLU(cfg.d_model, cfg.hidden)
-        self.tap_attn_out = Tap()
-        self.tap_resid_post = Tap()
+        self.tap_attn_out = make_tap()
+        self.tap_resid_post = make_tap()
 
     def forward(self, x, cos, sin, cache=None, same_doc=None):
         x = x + self.tap_attn_out(self.attn(self.norm1(x), cos, sin, cache, same_doc))
@@ -76,7 +76,20 @@ class Transformer(nn.Module):
         for name, p in self.named_parameters():
             if name.endswith(("o_proj.weight", "down.weight")):
                 nn.init.normal_(p, 0.0, cfg.init_std / math.sqrt(2 * cfg.n_layers))
-        assign_tap_names(self)
+        self._share_layers()
+        name_taps(self)
+
+    def _share_layers(self) -> None:
+        """cfg.shared_layers: block i takes block j's Linear Parameters (the same objects),
+        norms stay per block; each application keeps its own cache slot (layer index i)."""
+        for i, j in enumerate(self.cfg.shared_layers):
+            if i == j:
+                continue
+            linears = {n: m for n, m in self.blocks[j].named_modules() if isinstance(m, nn.Linear)}
+            for n, m in self.blocks[i].named_modules():
+                if n in linears:
+                    m.weight = linears[n].weight
+                    m.bias = linears[n].bias
 
     def _init(self, m):
         if isinstance(m, (nn.Linear, nn.Embedding)):

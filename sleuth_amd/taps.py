@@ -1,71 +1,123 @@
-"""Taps: named identity points the analyzer can listen on or replace.
+"""Named observation points ("taps") of the attention module.
 
-Same contract as sleuth/forge/model/taps.py:47-102: a Tap calls each listener as
-fn(name, tensor) and a returned tensor replaces the activation; listen() attaches
-listeners by fnmatch pattern for the duration of a `with` block. The attention module
-exposes attn.q / attn.k ([B,H,T,hd] after RoPE), attn.pattern ([B,H,T,S] probabilities;
-listening forces the explicit torch path) and attn.z ([B,T,H,hd] per-head output).
+The module exposes four of them (names relative to the module; the reference's tap
+contract, sleuth/forge/model/taps.py:22-34):
+    q        queries after norm + RoPE          [B, H, T, hd]
+    k        keys after norm + RoPE (KV heads)  [B, K, T, hd]
+    pattern  attention probabilities           [B, H, T, S]  (listening forces the torch path)
+    z        per-head attention output         [B, T, H, hd]
+A listener is called as fn(name, tensor); a tensor it returns replaces the activation.
+
+Interoperability: when the module runs inside Sleuth (the package `sleuth.forge.model.taps`
+is importable), `tap_class()` is the host's own Tap type, so the host's isinstance-based
+discovery (taps.py:68-102: assign_tap_names / listen) sees the attention taps like any
+other. Outside Sleuth the module uses `Tap` below. The helpers in this file (name_taps,
+listen, tap_names) find taps by duck typing -- any module with `name` and a `listeners`
+list -- so they work on either kind.
 """
 
 from __future__ import annotations
 
 import fnmatch
-from contextlib import contextmanager
+import functools
+import importlib
+from contextlib import ExitStack, contextmanager
 from typing import Callable, Iterator
 
 import torch
 from torch import nn
 
 Listener = Callable[[str, torch.Tensor], "torch.Tensor | None"]
+HOST_TAPS_MODULE = "sleuth.forge.model.taps"
 
 
 class Tap(nn.Module):
-    def __init__(self):
+    """Identity module with a name; `listeners` is a plain list so that a host analyzer
+    that appends to it (the reference's protocol) and `listen()` below both work."""
+
+    def __init__(self) -> None:
         super().__init__()
         self.name = "<unnamed>"
         self.listeners: list[Listener] = []
 
     @property
     def active(self) -> bool:
-        return bool(self.listeners)
+        return len(self.listeners) > 0
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        for fn in self.listeners:
-            out = fn(self.name, x)
-            if out is not None:
-                x = out
+        if not self.listeners:
+            return x
+        for fn in tuple(self.listeners):   # a listener may detach itself
+            replaced = fn(self.name, x)
+            x = x if replaced is None else replaced
         return x
 
+    def extra_repr(self) -> str:
+        return repr(self.name)
 
-def assign_tap_names(model: nn.Module) -> None:
-    """blocks.3.attn.tap_z -> blocks.3.attn.z"""
+
+@functools.lru_cache(maxsize=None)
+def tap_class() -> type:
+    """The Tap type new modules are built with: the host's when Sleuth is importable,
+    else this file's. Cached; tests that swap the host call tap_class.cache_clear()."""
+    try:
+        host = importlib.import_module(HOST_TAPS_MODULE)
+    except ImportError:
+        return Tap
+    cls = getattr(host, "Tap", None)
+    return cls if isinstance(cls, type) and issubclass(cls, nn.Module) else Tap
+
+
+def make_tap() -> nn.Module:
+    return tap_class()()
+
+
+def is_tap(m: nn.Module) -> bool:
+    return isinstance(getattr(m, "listeners", None), list) and hasattr(m, "name")
+
+
+def tap_active(t: nn.Module) -> bool:
+    """Whether anything listens on t (either kind of tap)."""
+    return bool(getattr(t, "listeners", None))
+
+
+def _iter_taps(model: nn.Module) -> Iterator[tuple[str, nn.Module]]:
     for path, m in model.named_modules():
-        if isinstance(m, Tap):
-            parts = path.split(".")
-            parts[-1] = parts[-1].removeprefix("tap_")
-            m.name = ".".join(parts)
+        if is_tap(m):
+            yield path, m
 
 
-def find_taps(model: nn.Module, pattern: str) -> list[Tap]:
-    taps = [m for m in model.modules() if isinstance(m, Tap) and fnmatch.fnmatchcase(m.name, pattern)]
-    if not taps:
-        raise KeyError(f"no tap matches {pattern!r}")
-    return taps
+def name_taps(model: nn.Module) -> None:
+    """Name every tap after its place in the tree, the attribute's `tap_` prefix dropped:
+    blocks.3.attn.tap_z is named blocks.3.attn.z (the reference's naming rule)."""
+    for path, t in _iter_taps(model):
+        head, _, leaf = path.rpartition(".")
+        if leaf.startswith("tap_"):
+            leaf = leaf[len("tap_"):]
+        t.name = f"{head}.{leaf}" if head else leaf
+
+
+assign_tap_names = name_taps   # the reference's name for the same operation
 
 
 def tap_names(model: nn.Module) -> list[str]:
-    return [m.name for m in model.modules() if isinstance(m, Tap)]
+    return [t.name for _, t in _iter_taps(model)]
+
+
+def find_taps(model: nn.Module, pattern: str) -> list[nn.Module]:
+    hits = [t for _, t in _iter_taps(model) if fnmatch.fnmatchcase(t.name, pattern)]
+    if not hits:
+        raise KeyError(f"no tap matches {pattern!r}")
+    return hits
 
 
 @contextmanager
 def listen(model: nn.Module, listeners: dict[str, Listener]) -> Iterator[None]:
-    attached: list[tuple[Tap, Listener]] = []
-    try:
+    """Attach fn to every tap whose name matches its pattern for the `with` block; every
+    attachment is undone on exit, also when the block raises."""
+    with ExitStack() as undo:
         for pattern, fn in listeners.items():
-            for tap in find_taps(model, pattern):
-                tap.listeners.append(fn)
-                attached.append((tap, fn))
+            for t in find_taps(model, pattern):
+                t.listeners.append(fn)
+                undo.callback(t.listeners.remove, fn)
         yield
-    finally:
-        for tap, fn in attached:
-            tap.listeners.remove(fn)

@@ -220,6 +220,31 @@ def test_decode_ragged_many_rows(B):
     assert max_abs(got, ref) <= 2e-2
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_persistent_verify_row_blocks_with_early_returns(dtype):
+    """Device lengths (the persistent grid), T = 4 with G = 3 (12 query rows: row blocks of
+    8 and 4), window 40 and 64-key chunks. The two row blocks see different key ranges, and
+    the lengths put a chunk boundary just past row block 0's last key (L = 321) and just
+    before row block 1's first key (L = 553), so units return early without a block barrier:
+    the path on which the block's next work ticket must not be overwritten before every wave
+    has read the previous one. Equal to the oracle, and the uniform-length case equal bit
+    for bit to the dense grid of the host position."""
+    B, H, K, D, T = 6, 12, 4, 64, 4
+    lens = [44, 321, 553, 617, 1000, 257]
+    got, ref = _decode_case(77, dtype, B, H, K, D, T, lens, 40, chunk=64)
+    assert max_abs(got, ref) <= tol(dtype)
+    g = gen(78)
+    L = 321
+    kc = randn(g, B, K, 400, D, dtype=dtype).to(DEV)
+    vc = randn(g, B, K, 400, D, dtype=dtype).to(DEV)
+    q = randn(g, B, H, T, D, dtype=dtype).to(DEV)
+    dense = ops().attn_decode(q, kc, vc, scale=0.125, pos=L - T, window=40, chunk=64)
+    rp = torch.full((B,), L - T, dtype=torch.int32, device=DEV)
+    for _ in range(3):
+        persistent = ops().attn_decode(q, kc, vc, scale=0.125, row_pos=rp, max_kv_len=400, window=40, chunk=64)
+        assert torch.equal(dense, persistent)
+
+
 # ------------------------------------------------------------------ MTP drafter attention
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("H,K,D", [(8, 2, 128), (8, 1, 256)])

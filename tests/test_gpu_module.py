@@ -16,6 +16,7 @@ from helpers import max_abs
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
 DEV = "cuda"
+POISON = 1e4
 
 
 def _modules():
@@ -51,6 +52,8 @@ def _run_layer(dtype, d_model, H, K, hd, theta, steps, B=1, window=0, qk_norm=Tr
     a.tap_z.listeners.append(lambda n, t: seen.__setitem__("z", t.clone()))
     max_len = pos_start + sum(steps) + 8 if lens is None else max(lens) + sum(steps) + 8
     cache = KVCache([(K, hd)], B, max_len, DEV, dtype)
+    cache.k[0].fill_(POISON)   # every position a row has not stored: a kernel that reads
+    cache.v[0].fill_(POISON)   # past its row's length gives a visibly wrong output
     ocache = oracle.KVCache([(K, hd)], B, max_len, "cpu", torch.float32)
     cos_t, sin_t = oracle.rope_tables(hd, max_len, theta)
     g = torch.Generator().manual_seed(seed + 1)
@@ -99,20 +102,17 @@ def _run_layer(dtype, d_model, H, K, hd, theta, steps, B=1, window=0, qk_norm=Tr
     return results
 
 
-def _downstream_argmax_ok(got, ref, vocab=256, seed=0):
-    """Logits = y @ W (W random); the argmax must agree on every row whose reference
-    top-2 margin exceeds the Cauchy-Schwarz bound on the logit error. Returns the
-    fraction of rows that were decided that way."""
-    g = torch.Generator().manual_seed(seed)
-    Bt = got.shape[0] * got.shape[1]
-    yg, yr = got.reshape(Bt, -1).double(), ref.reshape(Bt, -1).double()
-    W = torch.randn(yg.shape[1], vocab, generator=g, dtype=torch.float64) / math.sqrt(yg.shape[1])
-    lg, lr = yg @ W, yr @ W
-    bound = (yg - yr).norm(dim=1) * W.norm(dim=0).max()
-    top2 = lr.topk(2, dim=1).values
-    decided = (top2[:, 0] - top2[:, 1]) > 2 * bound
-    assert torch.equal(lg.argmax(1)[decided], lr.argmax(1)[decided])
-    return decided.double().mean().item()
+def _downstream_argmax_ok(got, ref):
+    """Downstream-logit argmax agreement (the north star's bf16 criterion), from helpers:
+    every row whose reference top-2 margin is at least 1% of the logits' RMS must pick the
+    same token; the rows below that margin are counted, and at most 10% may be."""
+    from helpers import downstream_argmax
+
+    r = downstream_argmax(got, ref)
+    print(f"downstream argmax: {r}")
+    assert r["mismatched"] == 0, r
+    assert r["near_ties"] <= 0.1 * r["rows"], r
+    return True
 
 
 def test_config1_fp32_prefill_then_64_decode_steps():
@@ -129,7 +129,7 @@ def test_config2_bf16_decode():
     res = _run_layer(torch.bfloat16, 768, 12, 4, 64, 1e4, [1] * 4, B=16, pos_start=2048)
     for got, ref, path in res:
         assert path == "hip-decode" and max_abs(got, ref) <= 2e-2
-        assert _downstream_argmax_ok(got, ref) >= 0.5
+        assert _downstream_argmax_ok(got, ref)
 
 
 def test_config3_bf16_prefill_and_decode():
@@ -139,7 +139,7 @@ def test_config3_bf16_prefill_and_decode():
     assert [r[2] for r in res] == ["hip-prefill", "hip-decode", "hip-decode"]
     for got, ref, _ in res:
         assert max_abs(got, ref) <= 2e-2
-        assert _downstream_argmax_ok(got, ref) >= 0.5
+        assert _downstream_argmax_ok(got, ref)
 
 
 def test_config4_ragged_decode():
@@ -148,7 +148,7 @@ def test_config4_ragged_decode():
     res = _run_layer(torch.bfloat16, 1024, 16, 8, 128, 1e6, [1, 1], B=8, lens=lens)
     for got, ref, path in res:
         assert path == "hip-decode" and max_abs(got, ref) <= 2e-2
-        assert _downstream_argmax_ok(got, ref) >= 0.5
+        assert _downstream_argmax_ok(got, ref)
 
 
 @pytest.mark.parametrize("window", [1024, 0])
@@ -158,7 +158,7 @@ def test_config5_mtp_verify(window):
     res = _run_layer(torch.bfloat16, 2048, 8, 1, 256, 1e6, [4, 4], B=8, window=window, pos_start=8192)
     for got, ref, path in res:
         assert path == "hip-decode" and max_abs(got, ref) <= 2e-2
-        assert _downstream_argmax_ok(got, ref) >= 0.5
+        assert _downstream_argmax_ok(got, ref)
 
 
 def test_v_norm_and_no_qk_norm():
@@ -210,18 +210,21 @@ def test_bf16_kv_cache_close_to_full_forward():
 
 
 def test_graph_generation_matches_eager():
-    """tests/test_cuda_graph.py:64-78: greedy tokens with HIP graphs = without, across
-    two length buckets, and the graphs are reused by the next call."""
-    from sleuth_amd.generate import generate
+    """tests/test_cuda_graph.py:64-78: greedy tokens with HIP graphs = without, from a short
+    context to the end of the cache; one graph serves every length (the kernels read the live
+    length on the device) and is reused by the next call."""
+    from sleuth_amd.generate import _decoders, generate
 
     m = _tiny(layer_types=["sliding", "full", "sliding"], sliding_window=8, max_seq_len=96).to(DEV, torch.bfloat16)
     prompt = [1, 5, 9, 13]
     eager = generate(m, prompt, 80)
     graph = generate(m, prompt, 80, cuda_graph=True)
     assert graph.new_ids == eager.new_ids
-    assert graph.stats["graphs"] == [64, 96]
+    assert graph.stats["graph_replays"] == 79
+    (dec,) = _decoders[m].values()
+    assert dec.recorded
     again = generate(m, prompt, 80, cuda_graph=True)
-    assert again.new_ids == eager.new_ids
+    assert again.new_ids == eager.new_ids and dec.replays == 2 * 79
 
 
 @pytest.mark.parametrize("cuda_graph", [False, True])
@@ -264,16 +267,19 @@ def test_taps_on_the_hip_path():
         assert not torch.allclose(base, ablated)
 
 
-def test_static_step_equals_normal_step_on_gpu():
-    """A static (graph-ready) step of 5 tokens == the normal path (tests/test_cuda_graph.py:81-95)."""
-    from sleuth_amd.kv_cache import StaticKVCache
+@pytest.mark.parametrize("host_cache", [False, True])
+def test_static_step_equals_normal_step_on_gpu(host_cache):
+    """A static (graph-ready) step of 5 tokens == the normal path (tests/test_cuda_graph.py:81-95),
+    with the product cache and with the host's StaticKVCache protocol."""
+    from host_protocol import HostStaticKVCache
+    from sleuth_amd.kv_cache import KVCache
 
     m = _tiny(layer_types=["sliding", "full", "sliding"], sliding_window=8).to(DEV)
     ids = torch.randint(0, 200, (1, 30), device=DEV)
     shapes = [(m.cfg.attn_spec(i).kv_heads, m.cfg.attn_spec(i).head_dim) for i in range(m.cfg.n_layers)]
     with torch.no_grad():
         full = m(ids).logits[0]
-        st = StaticKVCache(shapes, 1, 96, DEV, torch.float32, tokens_per_step=5)
+        st = (HostStaticKVCache if host_cache else KVCache)(shapes, 1, 96, DEV, torch.float32, tokens_per_step=5)
         m(ids[:, :20], cache=st)
         st.length, st.static = 32, True
         st.pos_t.fill_(20)
@@ -303,9 +309,11 @@ def test_fused_qkv_projection_matches_separate():
         finally:
             h.remove()
 
+    from sleuth_amd.attention import _FUSED_QKV
+
     with torch.no_grad():
         fused = a(x, cos, sin)
-        assert a._qkv_w is not None and a.q_proj.weight.data_ptr() == a._qkv_w.data_ptr()
+        assert a.q_proj.weight.data_ptr() == _FUSED_QKV[a.q_proj.weight].w.data_ptr()
         assert max_abs(fused.float().cpu(), separate().float().cpu()) <= 2e-2
         a.k_proj.weight.mul_(2.0)
         fused2 = a(x, cos, sin)
@@ -386,3 +394,134 @@ def test_gated_attention_hip_matches_torch(dtype):
     cos_t, sin_t = oracle.rope_tables(32, 64, 1e6)
     for got, ref in _hip_against_cpu(m, d, (2, 64), cos_t, sin_t, 4, lambda T: "hip"):
         assert max_abs(got, ref) <= (1e-4 if dtype == torch.float32 else 2e-2)
+
+
+# ----------------------------------------------------------------------------- host objects
+def test_hip_path_on_the_hosts_caches():
+    """The drop-in on the host's own cache objects (tests/host_protocol.py: exactly the
+    protocol of kv_cache.py:25-138, no per-row lengths, no room check): a 40-token prefill,
+    a decode step, a 5-token verify rewound as the speculative decoder does, and a
+    graph-captured static step replayed at two positions -- each against the oracle."""
+    from host_protocol import HostStaticKVCache
+
+    Attention, ModelConfig, _ = _modules()
+    H, K, hd, d, max_len, tps = 16, 8, 128, 1024, 128, 5
+    cfg = ModelConfig(vocab_size=10, d_model=d, n_heads=H, n_kv_heads=K, head_size=hd, qk_norm=True,
+                      rope_theta=1e6, n_layers=1)
+    torch.manual_seed(7)
+    a = Attention(cfg, 0).eval()
+    with torch.no_grad():
+        a.q_norm.weight.copy_(1 + 0.1 * torch.randn(hd))
+        a.k_norm.weight.copy_(1 + 0.1 * torch.randn(hd))
+    a = a.to(DEV, torch.bfloat16)
+    rec = {}
+    for name in ("q", "k", "v"):
+        getattr(a, f"{name}_proj").register_forward_hook(lambda m, i, o, n=name: rec.__setitem__(n, o))
+    seen = {}
+    a.tap_z.listeners.append(lambda n, t: seen.__setitem__("z", t))
+    cache = HostStaticKVCache([(K, hd)], 1, max_len, DEV, torch.bfloat16, tokens_per_step=tps)
+    cache.k[0].fill_(POISON)
+    cache.v[0].fill_(POISON)
+    ocache = oracle.KVCache([(K, hd)], 1, max_len, "cpu", torch.float32)
+    cos_t, sin_t = oracle.rope_tables(hd, max_len, 1e6)
+    cos_d, sin_d = cos_t.to(DEV), sin_t.to(DEV)
+    qw, kw = a.q_norm.weight.detach().float().cpu(), a.k_norm.weight.detach().float().cpu()
+    g = torch.Generator().manual_seed(8)
+
+    def oracle_out(p0, T):
+        q = rec["q"].view(1, T, H, hd).transpose(1, 2).float().cpu()
+        k = rec["k"].view(1, T, K, hd).transpose(1, 2).float().cpu()
+        v = rec["v"].view(1, T, K, hd).transpose(1, 2).float().cpu()
+        c, s_ = cos_t[p0:p0 + T], sin_t[p0:p0 + T]
+        qn = oracle.head_norm_rope(q.bfloat16(), qw, cfg.norm_eps, c, s_).float()
+        ocache.k[0][:, :, p0:p0 + T] = oracle.head_norm_rope(k.bfloat16(), kw, cfg.norm_eps, c, s_).float()
+        ocache.v[0][:, :, p0:p0 + T] = v
+        kk, vv = ocache.k[0][:, :, :p0 + T], ocache.v[0][:, :, :p0 + T]
+        return oracle.sdpa(qn, kk, vv, p0, 0, a.scale).transpose(1, 2)
+
+    def eager(T):
+        p0 = cache.pos
+        x = torch.randn(1, T, d, generator=g).to(torch.bfloat16).to(DEV)
+        with torch.no_grad():
+            a(x, cos_d[p0:p0 + T], sin_d[p0:p0 + T], cache)
+        return seen["z"].float().cpu(), oracle_out(p0, T)
+
+    for T, path in ((40, "hip-prefill"), (1, "hip-decode")):
+        got, ref = eager(T)
+        assert a.last_path == path and max_abs(got, ref) <= 2e-2, (T, max_abs(got, ref))
+        cache.advance(T)
+    start = cache.pos
+    got, ref = eager(5)                      # verify of [pending] + 4 guesses ...
+    assert a.last_path == "hip-decode" and max_abs(got, ref) <= 2e-2
+    cache.advance(5)
+    cache.pos = start + 2                    # ... of which the caller keeps two
+    assert torch.all(cache.k[0][0, :, start + 5:] == POISON)
+
+    # graph-captured static step: positions pos_t .. pos_t + 4 on the device
+    x_buf = torch.zeros(1, tps, d, device=DEV, dtype=torch.bfloat16)
+
+    def static_step():
+        cache.new_step()
+        pos = cache.positions
+        return a(x_buf, cos_d.index_select(0, pos), sin_d.index_select(0, pos), cache)
+
+    cache.static, cache.length = True, 64
+    cache.pos_t.fill_(cache.pos)
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            static_step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_step()
+    assert a.last_path == "hip-decode"
+    for _ in range(2):
+        p0 = cache.pos
+        x_buf.copy_(torch.randn(1, tps, d, generator=g).to(torch.bfloat16))
+        cache.pos_t.fill_(p0)
+        graph.replay()
+        torch.cuda.synchronize()
+        got, ref = seen["z"].float().cpu(), oracle_out(p0, tps)
+        assert max_abs(got, ref) <= 2e-2, (p0, max_abs(got, ref))
+        cache.pos = p0 + 3                   # keep three of the five
+    cache.static = False
+
+
+@pytest.mark.parametrize("cuda_graph", [False, True])
+def test_shared_layers_on_gpu(cuda_graph):
+    """Looped layers (tests/test_shared_layers.py:44-54, reference transformer.py:215-228):
+    blocks 1-3 share one set of projection Parameters. The fused q/k/v buffer is built once
+    per set of Parameters and never again (eager and graph-captured decoding); chunked
+    decoding matches one pass; graph decoding gives the eager tokens, and both match the
+    torch path's first logits."""
+    from sleuth_amd.attention import _FusedQKV
+    from sleuth_amd.generate import generate
+    from sleuth_amd.kv_cache import KVCache
+
+    m = _tiny(n_layers=5, shared_layers=[0, 1, 1, 1, 4], max_seq_len=64).to(DEV, torch.bfloat16)
+    x = torch.randint(0, 200, (1, 24), device=DEV)
+    with torch.no_grad():
+        before = _FusedQKV.builds
+        full = m(x).logits.float()
+        assert _FusedQKV.builds - before == 3        # blocks 0, 1 (= 2 = 3) and 4
+        built = _FusedQKV.builds
+        cache = KVCache.for_model(m, 1)
+        parts = [m(x[:, :16], cache=cache).logits.float()]
+        parts += [m(x[:, i:i + 1], cache=cache).logits.float() for i in range(16, 24)]
+        assert (torch.cat(parts, 1) - full).abs().max().item() < 0.1
+        assert not torch.equal(cache.k[1], cache.k[2])
+        out = generate(m, [3, 1, 4, 1, 5], 30, cuda_graph=cuda_graph)
+        assert _FusedQKV.builds == built
+        if cuda_graph:
+            assert out.new_ids == generate(m, [3, 1, 4, 1, 5], 30).new_ids
+        import os
+
+        os.environ["SLEUTH_AMD_NO_HIP"] = "1"
+        try:
+            torch_logits = m(x).logits.float()
+        finally:
+            del os.environ["SLEUTH_AMD_NO_HIP"]
+        assert m.blocks[0].attn.last_path == "torch"
+        assert (torch_logits - full).abs().max().item() < 0.1

@@ -4,6 +4,8 @@ test_speculative.py), checked against the oracle."""
 
 from __future__ import annotations
 
+import sys
+
 import pytest
 import torch
 
@@ -11,9 +13,10 @@ import oracle
 from sleuth_amd.attention import Attention
 from sleuth_amd.config import ModelConfig
 from sleuth_amd.generate import generate, ngram_draft, speculative_generate
-from sleuth_amd.kv_cache import KVCache, StaticKVCache
+from host_protocol import HostKVCache, HostStaticKVCache, HostTap, host_assign_names, host_listen
+from sleuth_amd.kv_cache import KVCache
 from sleuth_amd.model import Transformer
-from sleuth_amd.taps import assign_tap_names, listen, tap_names
+from sleuth_amd.taps import Tap, assign_tap_names, listen, tap_class, tap_names
 
 VARIANTS = [
     dict(),
@@ -128,34 +131,44 @@ def test_cache_protocol():
     c.advance(3)
     with pytest.raises(ValueError, match="KV cache full"):
         c.update(0, torch.randn(2, 2, 8, 8), torch.randn(2, 2, 8, 8))
-    with pytest.raises(ValueError, match="KV cache full"):
-        c.check_room(8)
     h = c.token_history(2, "cpu")
     assert h.shape == (2, 10) and torch.all(h == -1)
+    c.set_lengths([2, 5])
+    assert c.ragged and c.pos == 5 and c.seq_lens.tolist() == [2, 5]
+    c.pos = 4                       # the speculative decoder's rewind moves every row
+    assert not c.ragged and c.seq_lens_host == [4, 4]
     c.reset()
     assert c.pos == 0
+    # one allocation holds every layer's K and V
+    assert c.k[1].untyped_storage().data_ptr() == c.v[0].untyped_storage().data_ptr()
 
 
-def test_static_cache_masks_and_positions():
-    """tests/test_cuda_graph.py:55-61 golden masks, on the product cache."""
-    c = StaticKVCache([(1, 4)], 1, 32, "cpu", torch.float32)
+@pytest.mark.parametrize("cls", [KVCache, HostStaticKVCache])
+def test_static_cache_masks_and_positions(cls):
+    """tests/test_cuda_graph.py:55-61 golden masks, on the product cache and the host stand-in."""
+    c = cls([(1, 4)], 1, 32, "cpu", torch.float32)
     c.length, c.static = 16, True
     c.pos_t.fill_(10)
     assert c.attn_mask().view(-1).tolist() == [True] * 11 + [False] * 5
     assert c.attn_mask(4).view(-1).nonzero().view(-1).tolist() == [7, 8, 9, 10]
-    c2 = StaticKVCache([(1, 4)], 1, 32, "cpu", torch.float32, tokens_per_step=3)
+    c2 = cls([(1, 4)], 1, 32, "cpu", torch.float32, tokens_per_step=3)
     c2.pos_t.fill_(5)
     assert c2.positions.tolist() == [5, 6, 7]
+    c2.new_step()
+    c2.pos_t.fill_(9)
+    assert c2.positions.tolist() == [9, 10, 11]
 
 
+@pytest.mark.parametrize("static_cls", [KVCache, HostStaticKVCache])
 @pytest.mark.parametrize("kw", [{}, {"layer_types": ["sliding", "full", "sliding"], "sliding_window": 8}])
-def test_static_decode_matches_normal_decode(kw):
-    """tests/test_cuda_graph.py:24-52 (static steps on the CPU, two length buckets)."""
+def test_static_decode_matches_normal_decode(kw, static_cls):
+    """tests/test_cuda_graph.py:24-52 (static steps on the CPU, two view lengths), with the
+    product cache and with the host's StaticKVCache protocol."""
     m = make(n_kv_heads=2, max_seq_len=96, **kw)
     ids = torch.randint(0, 300, (1, 40))
     shapes = [(m.cfg.attn_spec(i).kv_heads, m.cfg.attn_spec(i).head_dim) for i in range(m.cfg.n_layers)]
-    normal = KVCache(shapes, 1, 96, "cpu", torch.float32)
-    static = StaticKVCache(shapes, 1, 96, "cpu", torch.float32)
+    normal = HostKVCache(shapes, 1, 96, "cpu", torch.float32)
+    static = static_cls(shapes, 1, 96, "cpu", torch.float32)
     with torch.no_grad():
         a = m(ids[:, :5], cache=normal).logits[:, -1]
         b = m(ids[:, :5], cache=static).logits[:, -1]
@@ -213,6 +226,80 @@ def test_too_long_and_bad_configs_rejected():
         ModelConfig(vocab_size=10, d_model=64, n_heads=4, n_kv_heads=3)
     with pytest.raises(ValueError):
         ModelConfig(vocab_size=10, d_model=64, n_heads=4, layer_types=["sliding"] * 6)
+
+
+@pytest.mark.parametrize("kw", VARIANTS[:4])
+def test_module_runs_on_the_hosts_cache(kw):
+    """The host's KVCache (kv_cache.py:25-70, nothing more) drives the module like the
+    product cache: chunked prefill + decode give the same logits as one pass."""
+    m = make(**kw)
+    x = torch.randint(0, 300, (2, 24))
+    with torch.no_grad():
+        full = m(x).logits
+        host = HostKVCache.for_model(m, 2)
+        parts = [m(x[:, :9], cache=host).logits]
+        parts += [m(x[:, i:i + 1], cache=host).logits for i in range(9, 24)]
+    torch.testing.assert_close(torch.cat(parts, 1), full, atol=1e-5, rtol=1e-4)
+    assert host.pos == 24
+    with pytest.raises(ValueError, match="KV cache full"):
+        m.blocks[0].attn(torch.zeros(2, 30, 64), *m.rope_rows(0, 30)[m.blocks[0].kind], cache=HostKVCache.for_model(m, 2, 20))
+
+
+def test_module_taps_are_the_hosts_tap_type(monkeypatch):
+    """Inside Sleuth (sleuth.forge.model.taps importable) the module builds its taps from the
+    host's Tap class, so the host's isinstance-based naming and listen() find
+    blocks.*.attn.{q,k,pattern,z}; outside it, this package's Tap."""
+    import types
+
+    host = types.ModuleType("sleuth.forge.model.taps")
+    host.Tap = HostTap
+    for name in ("sleuth", "sleuth.forge", "sleuth.forge.model"):
+        monkeypatch.setitem(sys.modules, name, types.ModuleType(name))
+    monkeypatch.setitem(sys.modules, "sleuth.forge.model.taps", host)
+    tap_class.cache_clear()
+    try:
+        m = make(n_kv_heads=2, qk_norm=True)
+        assert isinstance(m.blocks[1].attn.tap_z, HostTap)
+        host_assign_names(m)
+        seen = []
+        rec = lambda name, t: seen.append((name, tuple(t.shape)))  # noqa: E731
+        x = torch.randint(0, 300, (1, 6))
+        with torch.no_grad():
+            base = m(x).logits
+            with host_listen(m, {f"blocks.*.attn.{n}": rec for n in ("q", "k", "pattern", "z")}):
+                m(x)
+            with host_listen(m, {"blocks.2.attn.z": lambda n, t: torch.zeros_like(t)}):
+                ablated = m(x).logits
+        names = {n for n, _ in seen}
+        assert names == {f"blocks.{i}.attn.{t}" for i in range(3) for t in ("q", "k", "pattern", "z")}
+        assert ("blocks.0.attn.pattern", (1, 4, 6, 6)) in seen and ("blocks.1.attn.z", (1, 6, 4, 16)) in seen
+        assert not torch.allclose(base, ablated)
+        # the package's own helpers find host taps too (duck typing)
+        assert "blocks.1.attn.k" in tap_names(m)
+    finally:
+        monkeypatch.undo()
+        tap_class.cache_clear()
+    assert tap_class() is Tap and isinstance(make().blocks[0].attn.tap_q, Tap)
+
+
+def test_shared_layers_each_application_has_its_own_cache_slot():
+    """tests/test_shared_layers.py:44-54: looped layers share Parameters, not cache slots."""
+    m = make(n_layers=5, shared_layers=[0, 1, 1, 1, 4])
+    b = m.blocks
+    assert b[2].attn.q_proj.weight is b[1].attn.q_proj.weight is b[3].attn.q_proj.weight
+    assert b[4].attn.q_proj.weight is not b[1].attn.q_proj.weight
+    assert b[2].norm1.weight is not b[1].norm1.weight
+    x = torch.randint(0, 300, (1, 10))
+    with torch.no_grad():
+        full = m(x).logits
+        cache = KVCache.for_model(m, 1)
+        m(x[:, :6], cache=cache)
+        steps = [m(x[:, i:i + 1], cache=cache).logits for i in range(6, 10)]
+    torch.testing.assert_close(torch.cat(steps, 1), full[:, 6:], atol=1e-5, rtol=1e-5)
+    assert len(cache.k) == 5 and not torch.equal(cache.k[1], cache.k[2])
+    for bad in ([0, 1], [0, 2, 1, 1, 1], [0, 0, 1, 1, 1]):
+        with pytest.raises(ValueError):
+            ModelConfig(vocab_size=10, d_model=64, n_layers=5, n_heads=4, shared_layers=bad)
 
 
 def test_hip_gate_on_cpu():

@@ -369,3 +369,29 @@ def test_pins_catch_planted_mistakes():
     # drafter: the query's own position counted as stored / the window one key wider
     _raises(check_drafter, lambda q, k, v, n, win, sc: ref.drafter_attention(q, k, v, min(n + 1, k.shape[2]), win, sc))
     _raises(check_drafter, lambda q, k, v, n, win, sc: ref.drafter_attention(q, k, v, n, win + 1 if win else 0, sc))
+
+
+def test_downstream_argmax_check_has_teeth():
+    """The GPU tests' downstream-argmax criterion (helpers.downstream_argmax): bf16 rounding
+    of a correct output passes it; plausible kernel mistakes, planted here in the oracle on
+    the CPU, fail it."""
+    from helpers import downstream_argmax
+
+    g = torch.Generator().manual_seed(5)
+    B, H, K, T, S, D = 4, 8, 2, 16, 300, 64
+    q = torch.randn(B, H, T, D, generator=g)
+    k = torch.randn(B, K, S, D, generator=g)
+    v = torch.randn(B, K, S, D, generator=g)
+    sc = D ** -0.5
+    ref = oracle.sdpa(q, k, v, S - T, 0, sc).transpose(1, 2)
+    r = downstream_argmax(ref.bfloat16().float(), ref)
+    assert r["mismatched"] == 0 and r["near_ties"] <= 0.1 * r["rows"], r
+    planted = {
+        "scale squared": oracle.sdpa(q, k, v, S - T, 0, sc * sc),
+        "window off by one": oracle.sdpa(q, k, v, S - T, S - T, sc),
+        "last key dropped": oracle.sdpa(q, k[:, :, :-1], v[:, :, :-1], S - T - 1, 0, sc),
+        "GQA map h % K": oracle.sdpa(q, k[:, torch.arange(H) % K], v[:, torch.arange(H) % K], S - T, 0, sc),
+    }
+    for name, wrong in planted.items():
+        r = downstream_argmax(wrong.transpose(1, 2), ref)
+        assert r["mismatched"] > 0, (name, r)
