@@ -64,13 +64,20 @@ class _FusedQKV:
 
     builds = 0   # buffers built so far in this process (tests check that tied layers share one)
 
-    def __init__(self, ids, state, w, b):
+    def __init__(self, owner, ids, state, w, b):
+        self.owner = weakref.ref(owner)
         self.ids, self.state, self.w, self.b = ids, state, w, b
 
 
-# keyed by the q_proj weight Parameter: one buffer per set of Parameters, whichever modules
-# hold them; the entry goes away with the Parameter
-_FUSED_QKV: "weakref.WeakKeyDictionary[torch.Tensor, _FusedQKV]" = weakref.WeakKeyDictionary()
+# keyed by id() of the q_proj weight Parameter (tensors compare elementwise, so they cannot be
+# dict keys by value): one buffer per set of Parameters, whichever modules hold them; the
+# entry is dropped when that Parameter is collected
+_FUSED_QKV: dict[int, _FusedQKV] = {}
+
+
+def fused_qkv_entry(weight: torch.Tensor) -> "_FusedQKV | None":
+    e = _FUSED_QKV.get(id(weight))
+    return e if e is not None and e.owner() is weight else None
 
 
 class Attention(nn.Module):
@@ -124,7 +131,7 @@ class Attention(nn.Module):
         params = tuple(t for m in mods for t in (m.weight, m.bias) if t is not None)
         ids = tuple(id(t) for t in params)
         state = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in params)
-        entry = _FUSED_QKV.get(mods[0].weight)
+        entry = fused_qkv_entry(mods[0].weight)
         if entry is not None and entry.ids == ids and entry.state == state:
             return F.linear(x, entry.w, entry.b)
         if entry is not None and entry.ids != ids:
@@ -146,7 +153,10 @@ class Attention(nn.Module):
                     m.bias.data = b[off:off + n]
                 off += n
         state = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in params)
-        _FUSED_QKV[mods[0].weight] = _FusedQKV(ids, state, w, b)
+        key = id(mods[0].weight)
+        if key not in _FUSED_QKV:
+            weakref.finalize(mods[0].weight, _FUSED_QKV.pop, key, None)
+        _FUSED_QKV[key] = _FusedQKV(mods[0].weight, ids, state, w, b)
         _FusedQKV.builds += 1
         return F.linear(x, w, b)
 

@@ -42,7 +42,7 @@ def ops():
 def _argmax_ok(got, ref):
     r = downstream_argmax(got, ref)
     print(f"downstream argmax: {r}", flush=True)
-    assert r["mismatched"] == 0 and r["near_ties"] <= 0.1 * r["rows"], r
+    assert r["mismatched"] == 0 and r["near_ties"] <= max(2, 0.1 * r["rows"]), r
 
 
 def _gains(g, D):

@@ -105,13 +105,13 @@ def _run_layer(dtype, d_model, H, K, hd, theta, steps, B=1, window=0, qk_norm=Tr
 def _downstream_argmax_ok(got, ref):
     """Downstream-logit argmax agreement (the north star's bf16 criterion), from helpers:
     every row whose reference top-2 margin is at least 1% of the logits' RMS must pick the
-    same token; the rows below that margin are counted, and at most 10% may be."""
+    same token; the rows below that margin are counted, and at most 10% (or 2) may be."""
     from helpers import downstream_argmax
 
     r = downstream_argmax(got, ref)
     print(f"downstream argmax: {r}")
     assert r["mismatched"] == 0, r
-    assert r["near_ties"] <= 0.1 * r["rows"], r
+    assert r["near_ties"] <= max(2, 0.1 * r["rows"]), r
     return True
 
 
@@ -309,11 +309,11 @@ def test_fused_qkv_projection_matches_separate():
         finally:
             h.remove()
 
-    from sleuth_amd.attention import _FUSED_QKV
+    from sleuth_amd.attention import fused_qkv_entry
 
     with torch.no_grad():
         fused = a(x, cos, sin)
-        assert a.q_proj.weight.data_ptr() == _FUSED_QKV[a.q_proj.weight].w.data_ptr()
+        assert a.q_proj.weight.data_ptr() == fused_qkv_entry(a.q_proj.weight).w.data_ptr()
         assert max_abs(fused.float().cpu(), separate().float().cpu()) <= 2e-2
         a.k_proj.weight.mul_(2.0)
         fused2 = a(x, cos, sin)
