@@ -1188,27 +1188,33 @@ extern "C" int forge_attn_decode_chunk(int dtype, int B, int T, int H, int K, in
   return auto_chunk(dtype, B, T, H, K, D, max_kv_len);
 }
 
+// Workspace of a call with `slots` (row, chunk) partials: fp32 (m, l) pairs, fp32 partial
+// outputs, and the persistent grid's work ticket.
+static size_t workspace_for(int64_t slots, int D) {
+  const size_t ml = ((size_t)slots * sizeof(float2) + 255) / 256 * 256;
+  const size_t o = ((size_t)slots * D * sizeof(float) + 255) / 256 * 256;
+  return ml + o + 256;
+}
+
 extern "C" size_t forge_attn_decode_workspace_bytes(int dtype, int B, int T, int H, int K,
                                                     int D, int64_t max_kv_len, int chunk) {
   if (chunk <= 0) chunk = (K > 0 && H % K == 0) ? auto_chunk(dtype, B, T, H, K, D, max_kv_len) : 64;
   const int64_t max_chunks = (max_kv_len + chunk - 1) / chunk;
   if (max_chunks < 2) return 0;
-  const int64_t slots = (int64_t)B * H * T * max_chunks;
-  const size_t ml = ((size_t)slots * sizeof(float2) + 255) / 256 * 256;
-  const size_t o = ((size_t)slots * D * sizeof(float) + 255) / 256 * 256;
-  return ml + o + 256;  // + the persistent grid's work ticket
+  return workspace_for((int64_t)B * H * T * max_chunks, D);
 }
 
-extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, const void* q,
-                                 int64_t sqb, int64_t sqh, int64_t sqt, const float* q_weight,
-                                 float eps, int flags, const float* cos, const float* sin,
-                                 int64_t s_cos_b, int64_t s_cos_t, const void* k_cache,
-                                 const void* v_cache, int64_t skb, int64_t skh, int64_t sks,
-                                 int64_t max_len, const int32_t* row_pos, const int64_t* pos_dev,
-                                 int64_t pos0, int64_t max_kv_len, int window, float scale,
-                                 int chunk, void* out, int64_t sob, int64_t sot, int64_t soh,
-                                 void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
+namespace {
+
+// Checks the arguments of a decode call and fills everything of p but the workspace.
+// Returns 0, or the status of set_error.
+int decode_setup(SplitParams& p, int dtype, int B, int T, int H, int K, int D, const void* q,
+                 int64_t sqb, int64_t sqh, int64_t sqt, const float* q_weight, float eps,
+                 int flags, const float* cos, const float* sin, int64_t s_cos_b, int64_t s_cos_t,
+                 const void* k_cache, const void* v_cache, int64_t skb, int64_t skh, int64_t sks,
+                 int64_t max_len, const int32_t* row_pos, const int64_t* pos_dev, int64_t pos0,
+                 int64_t max_kv_len, int window, float scale, int chunk, void* out, int64_t sob,
+                 int64_t sot, int64_t soh) {
   if (dtype != FORGE_F32 && dtype != FORGE_BF16 && dtype != FORGE_F16)
     return set_error("unknown dtype code");
   if (B <= 0 || T <= 0 || H <= 0 || K <= 0) return set_error("sizes must be positive");
@@ -1234,7 +1240,7 @@ extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, c
   if (chunk <= 0) chunk = auto_chunk(dtype, B, T, H, K, D, chunk_span(max_kv_len, window));
   if (chunk % kpi) return set_error("chunk must be a multiple of the keys per block iteration");
 
-  SplitParams p{};
+  p = SplitParams{};
   p.q = q;
   p.sqb = sqb;
   p.sqh = sqh;
@@ -1271,22 +1277,56 @@ extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, c
   p.soh = soh;
   p.vec_tables = ((uintptr_t)q_weight | (uintptr_t)cos | (uintptr_t)sin) % 16 == 0 &&
                  (cos == nullptr || (s_cos_b % 4 == 0 && s_cos_t % 4 == 0));
-  if (p.max_chunks > 1) {
-    const size_t need = forge_attn_decode_workspace_bytes(dtype, B, T, H, K, D, max_kv_len, chunk);
-    if (!workspace || workspace_bytes < need) return set_error("workspace too small");
-    const int64_t slots = (int64_t)B * H * T * p.max_chunks;
-    const size_t ml = ((size_t)slots * sizeof(float2) + 255) / 256 * 256;
-    p.ws_ml = static_cast<float2*>(workspace);
-    p.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + ml);
-    const size_t o = ((size_t)slots * D * sizeof(float) + 255) / 256 * 256;
-    p.ws_ctr = reinterpret_cast<int*>(static_cast<char*>(workspace) + ml + o);
-  }
+  return 0;
+}
+
+// Workspace bytes the call set up in p needs (0: one chunk per row, no partials).
+size_t decode_need(const SplitParams& p, int D) {
+  return p.max_chunks > 1 ? workspace_for((int64_t)p.B * p.H * p.T * p.max_chunks, D) : 0;
+}
+
+// Points p's partials and work ticket into `ws` (at least decode_need bytes).
+void decode_bind(SplitParams& p, int D, void* ws) {
+  if (p.max_chunks < 2) return;
+  const int64_t slots = (int64_t)p.B * p.H * p.T * p.max_chunks;
+  const size_t ml = ((size_t)slots * sizeof(float2) + 255) / 256 * 256;
+  const size_t o = ((size_t)slots * D * sizeof(float) + 255) / 256 * 256;
+  p.ws_ml = static_cast<float2*>(ws);
+  p.ws_o = reinterpret_cast<float*>(static_cast<char*>(ws) + ml);
+  p.ws_ctr = reinterpret_cast<int*>(static_cast<char*>(ws) + ml + o);
+}
+
+int decode_launch(const SplitParams& p, int dtype, int D, hipStream_t s) {
+  if (use_verify_mfma(dtype, D, p.G))
+    return dtype == FORGE_BF16 ? launch_verify<bf16>(p, D, s) : launch_verify<f16>(p, D, s);
   const int rows = rows_per_block(p.rows_total);
-  hipStream_t s = (hipStream_t)stream;
-  if (mfma_path) return dtype == FORGE_BF16 ? launch_verify<bf16>(p, D, s) : launch_verify<f16>(p, D, s);
   switch (dtype) {
     case FORGE_F32: return launch_split<float>(p, D, rows, s);
     case FORGE_BF16: return launch_split<bf16>(p, D, rows, s);
     default: return launch_split<f16>(p, D, rows, s);
   }
+}
+
+}  // namespace
+
+extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, const void* q,
+                                 int64_t sqb, int64_t sqh, int64_t sqt, const float* q_weight,
+                                 float eps, int flags, const float* cos, const float* sin,
+                                 int64_t s_cos_b, int64_t s_cos_t, const void* k_cache,
+                                 const void* v_cache, int64_t skb, int64_t skh, int64_t sks,
+                                 int64_t max_len, const int32_t* row_pos, const int64_t* pos_dev,
+                                 int64_t pos0, int64_t max_kv_len, int window, float scale,
+                                 int chunk, void* out, int64_t sob, int64_t sot, int64_t soh,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  SplitParams p;
+  const int st = decode_setup(p, dtype, B, T, H, K, D, q, sqb, sqh, sqt, q_weight, eps, flags, cos,
+                              sin, s_cos_b, s_cos_t, k_cache, v_cache, skb, skh, sks, max_len,
+                              row_pos, pos_dev, pos0, max_kv_len, window, scale, chunk, out, sob,
+                              sot, soh);
+  if (st) return st;
+  const size_t need = decode_need(p, D);
+  if (need && (!workspace || workspace_bytes < need)) return set_error("workspace too small");
+  decode_bind(p, D, workspace);
+  return decode_launch(p, dtype, D, (hipStream_t)stream);
 }
