@@ -110,6 +110,29 @@ int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, const void* 
                       float scale, int chunk, void* out, int64_t sob, int64_t sot, int64_t soh,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Allocation-free forge_attn_decode (no counterpart in the reference). For callers that
+ * cannot allocate device memory: code under graph capture that may not call hipMalloc,
+ * tight serving loops, harnesses that forbid allocation. Same arguments and results as
+ * forge_attn_decode (bit for bit, same chunk) without the workspace: the split-K partials
+ * and the work ticket live in a device array inside the library, FORGE_NOALLOC_SCRATCH_BYTES
+ * per device, held from the library's load until the process ends. A call that needs more
+ * (forge_attn_decode_workspace_bytes > FORGE_NOALLOC_SCRATCH_BYTES) is rejected (< 0) before
+ * anything is launched. It calls no allocator. Every call on one device uses that device's
+ * one array: calls that may overlap on a device (other streams, no ordering between them)
+ * race; calls ordered on one stream do not.
+ */
+#define FORGE_NOALLOC_SCRATCH_BYTES (48 * 1024 * 1024)
+int forge_attn_decode_noalloc(int dtype, int B, int T, int H, int K, int D, const void* q,
+                              int64_t sqb, int64_t sqh, int64_t sqt, const float* q_weight,
+                              float eps, int flags, const float* cos, const float* sin,
+                              int64_t s_cos_b, int64_t s_cos_t, const void* k_cache,
+                              const void* v_cache, int64_t skb, int64_t skh, int64_t sks,
+                              int64_t max_len, const int32_t* row_pos, const int64_t* pos_dev,
+                              int64_t pos0, int64_t max_kv_len, int window, float scale,
+                              int chunk, void* out, int64_t sob, int64_t sot, int64_t soh,
+                              void* stream);
+
 /* Keys per split for a row span of max_kv_len keys (pure host function). T is accepted
  * for the signature but does not enter, so decode and verify steps of one layer agree. */
 int forge_attn_decode_chunk(int dtype, int B, int T, int H, int K, int D, int64_t max_kv_len);

@@ -25,6 +25,7 @@
 // a row's output does not depend on T or on the other rows in the call: a verify row
 // equals the decode of that token alone, bit for bit (same chunk).
 #include <limits.h>
+#include <stdio.h>
 
 #include <mutex>
 
@@ -1328,5 +1329,71 @@ extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, c
   const size_t need = decode_need(p, D);
   if (need && (!workspace || workspace_bytes < need)) return set_error("workspace too small");
   decode_bind(p, D, workspace);
+  return decode_launch(p, dtype, D, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------- allocation-free entry point
+// For callers that cannot allocate device memory (code under graph capture that may not call
+// hipMalloc, tight serving loops): the split-K partials and the work ticket live in this
+// file-scope device array instead of a caller-provided workspace. Every device that loads the
+// library holds its own copy until the process ends. Host code never uses the array's name as
+// an address: its device address is looked up once per device (hipGetSymbolAddress, with that
+// device current) and only that address goes to the kernels. All calls on one device share the
+// array, so calls that overlap on one device (different streams, no ordering) race on it.
+static __device__ __align__(256) unsigned char scratch[FORGE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+// The device address of `scratch` on the current device, looked up on first use there.
+void* scratch_address() {
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    addr[dev] = ptr;
+  }
+  return addr[dev];
+}
+
+}  // namespace
+
+extern "C" int forge_attn_decode_noalloc(int dtype, int B, int T, int H, int K, int D,
+                                         const void* q, int64_t sqb, int64_t sqh, int64_t sqt,
+                                         const float* q_weight, float eps, int flags,
+                                         const float* cos, const float* sin, int64_t s_cos_b,
+                                         int64_t s_cos_t, const void* k_cache,
+                                         const void* v_cache, int64_t skb, int64_t skh,
+                                         int64_t sks, int64_t max_len, const int32_t* row_pos,
+                                         const int64_t* pos_dev, int64_t pos0,
+                                         int64_t max_kv_len, int window, float scale, int chunk,
+                                         void* out, int64_t sob, int64_t sot, int64_t soh,
+                                         void* stream) {
+  clear_error();
+  SplitParams p;
+  const int st = decode_setup(p, dtype, B, T, H, K, D, q, sqb, sqh, sqt, q_weight, eps, flags, cos,
+                              sin, s_cos_b, s_cos_t, k_cache, v_cache, skb, skh, sks, max_len,
+                              row_pos, pos_dev, pos0, max_kv_len, window, scale, chunk, out, sob,
+                              sot, soh);
+  if (st) return st;
+  const size_t need = decode_need(p, D);
+  if (need > (size_t)FORGE_NOALLOC_SCRATCH_BYTES) {
+    char msg[200];
+    snprintf(msg, sizeof msg,
+             "forge_attn_decode_noalloc: this call needs %zu bytes of split-K scratch, more than "
+             "the %d the library holds (use forge_attn_decode with a workspace, or a larger chunk)",
+             need, FORGE_NOALLOC_SCRATCH_BYTES);
+    return set_error(msg);
+  }
+  if (need) {
+    void* ws = scratch_address();
+    if (!ws) return set_error("forge_attn_decode_noalloc: cannot find the scratch array on this device");
+    decode_bind(p, D, ws);   // the work ticket is zeroed by a kernel before the launch that uses it
+  }
   return decode_launch(p, dtype, D, (hipStream_t)stream);
 }

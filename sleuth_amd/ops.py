@@ -172,15 +172,10 @@ def decode_workspace_bytes(dtype: torch.dtype, B: int, T: int, H: int, K: int, D
     return lib().forge_attn_decode_workspace_bytes(_DTYPES[dtype], B, T, H, K, D, int(max_kv_len), int(chunk))
 
 
-def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *, scale: float,
-                pos: int | None = None, pos_dev: torch.Tensor | None = None,
-                row_pos: torch.Tensor | None = None, max_kv_len: int | None = None,
-                window: int = 0, q_weight: torch.Tensor | None = None, eps: float = 1e-6,
-                norm_q: bool = False, cos: torch.Tensor | None = None,
-                sin: torch.Tensor | None = None, chunk: int = 0, out: torch.Tensor | None = None,
-                workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """Split-K attention of the T new queries q [B,H,T,D] against the cache, whose rows
-    hold base_b + T valid keys (the new ones included). Returns [B,T,H,D]."""
+def _decode_args(q, k_cache, v_cache, scale, pos, pos_dev, row_pos, max_kv_len, window, q_weight,
+                 eps, norm_q, cos, sin, chunk, out, workspace):
+    """Host checks of a decode call; returns (C arguments up to `out`'s strides, out,
+    device, max_kv_len, chunk)."""
     B, H, T, D = q.shape
     Bc, K, max_len, Dc = k_cache.shape
     if Bc != B or Dc != D or v_cache.shape != k_cache.shape or H % K:
@@ -203,21 +198,52 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *
         out = torch.empty(B, T, H, D, dtype=q.dtype, device=dev)
     elif out.shape != (B, T, H, D) or out.dtype != q.dtype:
         raise ValueError(f"out must be [B,T,H,D] = {(B, T, H, D)} {q.dtype}")
-    dt = dtype_code(q)
     if chunk <= 0:  # from the cache's capacity, not this call's length: stable across steps
         chunk = decode_chunk(q.dtype, B, T, H, K, D, max_len, window)
-    need = lib().forge_attn_decode_workspace_bytes(dt, B, T, H, K, D, max_kv_len, chunk)
+    args = (dtype_code(q), B, T, H, K, D, _ptr(q), q.stride(0), q.stride(1), q.stride(2),
+            _ptr(w), float(eps), flags, _ptr(c), _ptr(s), s_b, s_t,
+            _ptr(k_cache), _ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
+            k_cache.stride(2), max_len, _ptr(rp), _ptr(pd), p0, max_kv_len,
+            int(window), float(scale), int(chunk),
+            _ptr(out), out.stride(0), out.stride(1), out.stride(2))
+    return args, out, dev, max_kv_len, chunk
+
+
+def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *, scale: float,
+                pos: int | None = None, pos_dev: torch.Tensor | None = None,
+                row_pos: torch.Tensor | None = None, max_kv_len: int | None = None,
+                window: int = 0, q_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                norm_q: bool = False, cos: torch.Tensor | None = None,
+                sin: torch.Tensor | None = None, chunk: int = 0, out: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Split-K attention of the T new queries q [B,H,T,D] against the cache, whose rows
+    hold base_b + T valid keys (the new ones included). Returns [B,T,H,D]."""
+    args, out, dev, max_kv_len, chunk = _decode_args(q, k_cache, v_cache, scale, pos, pos_dev, row_pos,
+                                                     max_kv_len, window, q_weight, eps, norm_q, cos, sin,
+                                                     chunk, out, workspace)
+    B, H, T, D = q.shape
+    need = lib().forge_attn_decode_workspace_bytes(args[0], B, T, H, k_cache.shape[1], D, max_kv_len, chunk)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    st = lib().forge_attn_decode(dt, B, T, H, K, D, _ptr(q), q.stride(0), q.stride(1), q.stride(2),
-                                 _ptr(w), float(eps), flags, _ptr(c), _ptr(s), s_b, s_t,
-                                 _ptr(k_cache), _ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
-                                 k_cache.stride(2), max_len, _ptr(rp), _ptr(pd), p0, max_kv_len,
-                                 int(window), float(scale), int(chunk),
-                                 _ptr(out), out.stride(0), out.stride(1), out.stride(2),
-                                 _ptr(workspace), ws_bytes, _stream(dev))
+    st = lib().forge_attn_decode(*args, _ptr(workspace), ws_bytes, _stream(dev))
     check(st, "forge_attn_decode")
+    return out
+
+
+def attn_decode_noalloc(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *, scale: float,
+                        out: torch.Tensor, pos: int | None = None, pos_dev: torch.Tensor | None = None,
+                        row_pos: torch.Tensor | None = None, max_kv_len: int | None = None,
+                        window: int = 0, q_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                        norm_q: bool = False, cos: torch.Tensor | None = None,
+                        sin: torch.Tensor | None = None, chunk: int = 0) -> torch.Tensor:
+    """attn_decode through forge_attn_decode_noalloc: the split-K partials live in the
+    library's own device array (at most NOALLOC_SCRATCH_BYTES), so the call allocates
+    nothing on the device; `out` must be given. Calls that may overlap on one GPU race on
+    that array."""
+    args, out, dev, _, _ = _decode_args(q, k_cache, v_cache, scale, pos, pos_dev, row_pos, max_kv_len,
+                                        window, q_weight, eps, norm_q, cos, sin, chunk, out, None)
+    check(lib().forge_attn_decode_noalloc(*args, _stream(dev)), "forge_attn_decode_noalloc")
     return out
 
 
@@ -291,5 +317,5 @@ def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: fl
     return out
 
 
-__all__ = ["head_norm_rope", "kv_append", "attn_decode", "attn_prefill", "decode_chunk",
+__all__ = ["head_norm_rope", "kv_append", "attn_decode", "attn_decode_noalloc", "attn_prefill", "decode_chunk",
            "decode_workspace_bytes", "attn_drafter", "prefill_supported", "dtype_code", "_lib"]
