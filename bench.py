@@ -9,7 +9,7 @@ step's algorithmic HBM bytes / step time (GB/s); tokens/s = 64 / (28 layers x st
 Beside it: C3 causal prefill (4 x 4096 tokens, bf16) in TFLOP/s, each dominant kernel's
 roofline fraction, and the oracle (torch SDPA on the CPU) timed on a bounded sample.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--extra]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-extra]
 """
 
 from __future__ import annotations
@@ -244,95 +244,119 @@ def read_traffic(name: str):
 
 
 # ----------------------------------------------------------------------------- CPU baseline
+CPU_WARMUP, CPU_RUNS = 3, 10   # 3 warm-up runs, then the median of >= 10
+
+
 def cpu_info() -> dict:
-    model = "unknown"
+    """The host CPU as the baseline reports it: model strings, logical and physical cores,
+    the affinity mask and the cgroup CPU quota."""
+    info = {"model": "unknown", "logical": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
     try:
+        cores, fields = set(), {}
+        phys = core = None
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
+            key, _, val = (x.strip() for x in line.partition(":"))
+            if key == "physical id":
+                phys = val
+            elif key == "core id":
+                core = val
+            elif key in ("model name", "cpu family", "model", "stepping", "vendor_id") and key not in fields:
+                fields[key] = val
+            elif not key and phys is not None:
+                cores.add((phys, core))
+                phys = core = None
+        if phys is not None:
+            cores.add((phys, core))
+        info["model"] = fields.get("model name", "unknown")
+        info["cpuid"] = {k: fields[k] for k in ("vendor_id", "cpu family", "model", "stepping") if k in fields}
+        info["physical_cores"] = len(cores) or None
     except OSError:
         pass
-    return {"model": model, "logical": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+    try:
+        import subprocess
+
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = (x.strip() for x in line.partition(":"))
+            if key in ("Model name", "Core(s) per socket", "Socket(s)", "Thread(s) per core"):
+                info[f"lscpu {key}"] = val
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()
+        info["cgroup_cpus"] = None if quota == "max" else round(int(quota) / int(period), 2)
+    except (OSError, ValueError):
+        pass
+    return info
 
 
-def cpu_baseline_decode(wl: DecodeWorkload, budget_s: float = 15.0) -> dict:
-    """The oracle's eager CPU path (torch SDPA on the host, bf16, one SDPA per row over
-    its prefix, attention.py:171-193) on the first rows of the same batch: add rows
-    until about budget_s of CPU work, then report GB/s of algorithmic bytes."""
+def _median_runs(fn) -> tuple[float, float, int]:
+    """CPU_WARMUP untimed calls, then CPU_RUNS timed ones: (median s, min s, runs)."""
+    for _ in range(CPU_WARMUP):
+        fn()
+    ts = []
+    for _ in range(CPU_RUNS):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2] if len(ts) % 2 else 0.5 * (ts[len(ts) // 2 - 1] + ts[len(ts) // 2]), ts[0], len(ts)
+
+
+def cpu_baseline_decode(wl: "DecodeWorkload", fp32_rows: int = 8) -> dict:
+    """The oracle's eager CPU path (torch SDPA on the host: attention.py:171-193 with the
+    one-rounding q norm + RoPE, one SDPA per ragged row over its prefix) over the whole C4
+    batch for one layer, in bf16; the same in fp32 over the first `fp32_rows` rows (the fp32
+    copy of the whole batch would need 17 GB of host memory). GB/s of algorithmic bytes."""
     import oracle
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    B, H, K, D = wl.B, wl.H, wl.K, wl.D
     q = oracle.head_norm_rope(wl.q.cpu(), wl.wq.cpu(), 1e-6, wl.cos.cpu(), wl.sin.cpu())
-    layer = wl.k_caches[0], wl.v_caches[0]
-    rows, total_b, total_t = 0, 0, 0.0
+    kc, vc = wl.k_caches[0].cpu(), wl.v_caches[0].cpu()
     s = torch.finfo(wl.dtype).bits // 8
-    for b in range(B):
-        L = wl.lens[b]
-        kc = layer[0][b:b + 1, :, :L].cpu()
-        vc = layer[1][b:b + 1, :, :L].cpu()
-        oracle.ragged_decode(q[b:b + 1], kc, vc, [L], wl.window, wl.scale)  # warm
-        t0 = time.perf_counter()
-        reps = 3
-        for _ in range(reps):
-            oracle.ragged_decode(q[b:b + 1], kc, vc, [L], wl.window, wl.scale)
-        dt = (time.perf_counter() - t0) / reps
-        rows += 1
-        total_t += dt
-        total_b += 2 * K * wl.visible(L) * D * s + 2 * H * wl.T * D * s
-        if total_t * (reps + 1) > budget_s:
-            break
-    # the same rows in fp32 (same algorithmic bytes), one run each after a warm-up
-    t32 = 0.0
-    for b in range(rows):
-        L = wl.lens[b]
-        kc = layer[0][b:b + 1, :, :L].float().cpu()
-        vc = layer[1][b:b + 1, :, :L].float().cpu()
-        q32 = q[b:b + 1].float()
-        oracle.ragged_decode(q32, kc, vc, [L], wl.window, wl.scale)
-        t0 = time.perf_counter()
-        oracle.ragged_decode(q32, kc, vc, [L], wl.window, wl.scale)
-        t32 += time.perf_counter() - t0
-    return {"value": round(total_b / total_t / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"rows 0..{rows - 1} of the C4 batch ({sum(wl.lens[:rows])} cached tokens), one layer, "
-                      f"bf16 torch SDPA on the host CPU, median-free mean of 3 runs per row",
-            "value_fp32": round(total_b / t32 / 1e9, 3),
+
+    def row_bytes(rows):
+        return sum(2 * wl.K * wl.visible(wl.lens[b]) * wl.D * s + 2 * wl.H * wl.T * wl.D * s for b in rows)
+
+    def run(rows, qq, kk, vv):
+        for b in rows:
+            L = wl.lens[b]
+            oracle.ragged_decode(qq[b:b + 1], kk[b:b + 1, :, :L], vv[b:b + 1, :, :L], [L], wl.window, wl.scale)
+
+    every = range(wl.B)
+    med, best, n = _median_runs(lambda: run(every, q, kc, vc))
+    few = range(min(fp32_rows, wl.B))
+    L32 = max(wl.lens[b] for b in few)
+    k32, v32 = kc[:len(few), :, :L32].float(), vc[:len(few), :, :L32].float()
+    med32, best32, _ = _median_runs(lambda: run(few, q.float(), k32, v32))
+    return {"value": round(row_bytes(every) / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the whole C4 batch for one layer ({sum(wl.lens)} cached tokens, 64 rows), bf16 torch SDPA "
+                      f"on the host CPU, one call per row; median of {n} runs after {CPU_WARMUP} warm-ups",
+            "value_best": round(row_bytes(every) / best / 1e9, 3),
+            "value_fp32": round(row_bytes(few) / med32 / 1e9, 3),
+            "value_fp32_sample": f"rows 0..{len(few) - 1} in fp32, median of {n} runs",
             "cpu": cpu_info()}
 
 
-def cpu_baseline_prefill(B, T, H, K, D, budget_s: float = 10.0) -> dict:
-    """torch SDPA (is_causal, enable_gqa) on the host in bf16 at the C3 shape, one
-    batch row (the sample), TFLOP/s."""
-    threads = min(16, len(os.sched_getaffinity(0)))
+def cpu_baseline_prefill(B, T, H, K, D) -> dict:
+    """torch SDPA (is_causal, enable_gqa) on the host at the full C3 shape (4 x 4096) in
+    bf16, and in fp32; TFLOP/s of the causal count."""
+    threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(2)
-    q = torch.randn(1, H, T, D, generator=g).bfloat16()
-    k = torch.randn(1, K, T, D, generator=g).bfloat16()
-    v = torch.randn(1, K, T, D, generator=g).bfloat16()
-    f = lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,  # noqa: E731
-                                                                  enable_gqa=True, scale=D ** -0.5)
-    f()
-    t0 = time.perf_counter()
-    n = 0
-    while time.perf_counter() - t0 < budget_s / 2 or n < 2:
-        f()
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    fl = 4.0 * D * H * T * (T + 1) / 2
-    q, k, v = q.float(), k.float(), v.float()  # the same in fp32
-    f()
-    t0 = time.perf_counter()
-    n32 = 0
-    while time.perf_counter() - t0 < budget_s / 4 or n32 < 2:
-        f()
-        n32 += 1
-    dt32 = (time.perf_counter() - t0) / n32
-    return {"value": round(fl / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"1 of the {B} batch rows ({T} tokens causal), bf16 torch SDPA, mean of {n} runs",
-            "value_fp32": round(fl / dt32 / 1e12, 4)}
+    q = torch.randn(B, H, T, D, generator=g).bfloat16()
+    k = torch.randn(B, K, T, D, generator=g).bfloat16()
+    v = torch.randn(B, K, T, D, generator=g).bfloat16()
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    fl = 4.0 * D * B * H * T * (T + 1) / 2
+    med, best, n = _median_runs(lambda: sdpa(q, k, v, is_causal=True, enable_gqa=True, scale=D ** -0.5))
+    q, k, v = q.float(), k.float(), v.float()
+    med32, _, _ = _median_runs(lambda: sdpa(q, k, v, is_causal=True, enable_gqa=True, scale=D ** -0.5))
+    return {"value": round(fl / med / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"the whole C3 prefill ({B} x {T} causal), bf16 torch SDPA on the host CPU, median of {n} "
+                      f"runs after {CPU_WARMUP} warm-ups",
+            "value_best": round(fl / best / 1e12, 4), "value_fp32": round(fl / med32 / 1e12, 4)}
 
 
 # ----------------------------------------------------------------------------- main
@@ -342,7 +366,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--extra", action="store_true", help="also print lines for configs C2, C3-decode, C5")
+    ap.add_argument("--no-extra", action="store_true", help="skip the reported configs C2, C3-decode, C5")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--config", default="", help="with --only extra: run only the configs whose name contains this")
     ap.add_argument("--only", choices=["decode", "prefill", "copy", "gemm", "sdpa", "qkv", "extra"],
@@ -387,8 +411,9 @@ def main() -> int:
     t_pstep = time_loop(pf.step, max(3, args.steps // 2), max(1, args.warmup // 2))
     t_pattn = time_loop(pf.attend, max(3, args.steps // 2), max(1, args.warmup // 2))
     p_tflops = pf.flops() / t_pattn / 1e12
-    print(f"[bench] C3 prefill step {t_pstep * 1e6:.1f} us, attention kernel {t_pattn * 1e6:.1f} us "
-          f"({p_tflops:.0f} TFLOP/s)", file=sys.stderr, flush=True)
+    p_step_tflops = pf.flops() / t_pstep / 1e12
+    print(f"[bench] C3 prefill step {t_pstep * 1e6:.1f} us ({p_step_tflops:.0f} TFLOP/s), attention kernel "
+          f"{t_pattn * 1e6:.1f} us ({p_tflops:.0f} TFLOP/s)", file=sys.stderr, flush=True)
     gemm = gemm_tflops(dev)
     print(f"[bench] bf16 8192^3 library GEMM {gemm:.0f} TFLOP/s", file=sys.stderr, flush=True)
     sdpa = sdpa_reference(dev)
@@ -420,6 +445,9 @@ def main() -> int:
         # comparison only (the roofline fraction uses the causal count)
         "prefill_tflops_full_s_convention": round(p_tflops * pf.flops_full_s() / pf.flops(), 1),
         "prefill_step_ms": round(t_pstep * 1e3, 4),
+        # the whole prefill step (forge_kv_append of the 4 x 4096 keys and values, then the
+        # attention kernel) against the same causal FLOP count
+        "prefill_step_tflops": round(p_step_tflops, 1),
         "prefill_warm_s": PREFILL_WARM_S,
         "prefill_config": "C3: 4 x 4096 causal, 16 q / 8 kv heads, head dim 128, bf16, QK-norm, RoPE theta 1e6",
         # the reference's own GPU attention call (torch SDPA, flash / memory-efficient backends)
@@ -444,8 +472,8 @@ def main() -> int:
         line["cpu_baseline_prefill"] = cpu_baseline_prefill(4, 4096, 16, 8, 128)
     else:
         line["cpu_baseline"] = None
-    if args.extra:
-        line["extra"] = extra_configs(dev, args)
+    if not args.no_extra:
+        line["configs"] = extra_configs(dev, args)
     print(json.dumps(line), flush=True)
     return 0
 
@@ -576,20 +604,34 @@ def run_only(args, dev) -> int:
     return 0
 
 
+EXTRA_CONFIGS = {
+    "C2_decode_b16_12q4kv_hd64_S2048": dict(lens=[2049] * 16, H=12, K=4, D=64, theta=1e4, n_layers=12),
+    "C3_decode_b32_16q8kv_hd128_S8192": dict(lens=[8192] * 32, H=16, K=8, D=128, theta=1e6, n_layers=1),
+    "C5_verify_b8_T4_8q1kv_hd256_global": dict(lens=[8196] * 8, H=8, K=1, D=256, theta=1e6, T=4, n_layers=12),
+    "C5_verify_b8_T4_8q1kv_hd256_window1024": dict(lens=[8196] * 8, H=8, K=1, D=256, theta=1e6, T=4,
+                                                   window=1024, n_layers=12),
+}
+# the rocprofv3 traffic summary of each (profiles/<name>.txt)
+EXTRA_TRAFFIC = {
+    "C2_decode_b16_12q4kv_hd64_S2048": "decode_c2_traffic",
+    "C3_decode_b32_16q8kv_hd128_S8192": "decode_c3_traffic",
+    "C5_verify_b8_T4_8q1kv_hd256_global": "verify_c5_global_traffic",
+    "C5_verify_b8_T4_8q1kv_hd256_window1024": "verify_c5_window1024_traffic",
+}
+
+
 def extra_configs(dev, args) -> dict:
-    """Configs C2, C3-decode and C5 (reported, no targets). Small working sets rotate
-    through several layer caches so the ~256 MB MALL does not serve them."""
+    """Configs C2, C3-decode and C5 (reported; BASELINE sets no target for them). Small
+    working sets rotate through several layer caches so the ~256 MB MALL does not serve
+    them. The roofline uses the attention call replayed from a HIP graph (how decode steps
+    run, and without the host's per-call launch cost, which exceeds these calls' GPU time);
+    the eager step (append + attention) and eager attention call are reported beside it."""
     out = {}
     dt = torch.bfloat16
-    for name, kw in {
-        "C2_decode_b16_12q4kv_hd64_S2048": dict(lens=[2049] * 16, H=12, K=4, D=64, theta=1e4, n_layers=12),
-        "C3_decode_b32_16q8kv_hd128_S8192": dict(lens=[8192] * 32, H=16, K=8, D=128, theta=1e6, n_layers=1),
-        "C5_verify_b8_T4_8q1kv_hd256_global": dict(lens=[8196] * 8, H=8, K=1, D=256, theta=1e6, T=4, n_layers=12),
-        "C5_verify_b8_T4_8q1kv_hd256_window1024": dict(lens=[8196] * 8, H=8, K=1, D=256, theta=1e6, T=4,
-                                                       window=1024, n_layers=12),
-    }.items():
+    for name, kw in EXTRA_CONFIGS.items():
         if args.config and args.config not in name:
             continue
+        kw = dict(kw)
         lens = kw.pop("lens")
         wl = DecodeWorkload(lens, dtype=dt, dev=dev, **kw)
         for i in range(len(wl.k_caches)):
@@ -599,11 +641,14 @@ def extra_configs(dev, args) -> dict:
         ta = time_loop(lambda: (wl.attend(), setattr(wl, "layer", (wl.layer + 1) % len(wl.k_caches))),
                        args.steps * 4, args.warmup)
         tg = time_graph(lambda i: wl.attend(i), len(wl.k_caches), args.steps, args.warmup)
+        gbs = wl.attend_bytes() / tg / 1e9
         out[name] = {"step_us": round(t * 1e6, 2), "step_GBs": round(wl.step_bytes() / t / 1e9, 1),
                      "attention_call_us": round(ta * 1e6, 2),
-                     "attention_GBs": round(wl.attend_bytes() / ta / 1e9, 1),
-                     "attention_graph_us": round(tg * 1e6, 2),
-                     "attention_graph_GBs": round(wl.attend_bytes() / tg / 1e9, 1), "chunk": wl.chunk}
+                     "attention_graph_us": round(tg * 1e6, 2), "chunk": wl.chunk,
+                     "layer_caches_rotated": len(wl.k_caches),
+                     "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": wl.attend_bytes(),
+                                  "traffic": read_traffic(EXTRA_TRAFFIC[name])}}
         print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
         del wl
         torch.cuda.empty_cache()

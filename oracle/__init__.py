@@ -12,8 +12,10 @@ from .attention_ref import (  # noqa: F401
     attention_forward,
     attention_mask,
     brute_attention,
+    eager_norm_rope,
     drafter_attention,
     explicit_attention,
+    gated_attention,
     head_norm_rope,
     ragged_decode,
     rms_norm,

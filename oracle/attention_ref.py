@@ -13,6 +13,9 @@ Parity pins (tests/test_oracle.py), chosen so that a plausible slip fails one of
   sdpa / explicit_attention  float64 brute force with explicit loops and the GQA map
                              kv = h // (H/K) (brute_attention); single-key and equal-key
                              closed forms; causality
+  gated_attention            float64 loops from the definition (partial RoPE on the first
+                             n_rot channels, q | gate split per head, sigmoid gate, causal
+                             at an offset), tests/test_oracle.py
   KVCache / StaticKVCache    chunked prefill + decode == full forward
                              (tests/test_model.py:61-69), static step == normal step
                              (tests/test_cuda_graph.py:24-52, 81-95)
@@ -285,3 +288,29 @@ def attention_forward(q, k, v, *, cos, sin, scale, eps=1e-6, q_weight=None, k_we
         kw = {"enable_gqa": True} if k.shape[1] != q.shape[1] else {}
         return F.scaled_dot_product_attention(q, k, v, attn_mask=cache.attn_mask(window), scale=scale, **kw)
     return sdpa(q, k, v, S - T, window, scale)
+
+
+# ----------------------------------------------------------------------------- gated attention
+def gated_attention(qg, k, v, *, cos, sin, n_rot, q_weight, k_weight, eps, k_past=None, v_past=None):
+    """Qwen3.5 gated attention after the projections (formats/qwen35.py:194-214).
+    qg [B,T,H,2hd]: each head's q_proj output as [q | gate]; k, v [B,T,K,hd] raw projections;
+    k_past/v_past [B,K,offset,hd]: keys and values already stored (normalised and rotated).
+    q and k: RMSNorm with gain (rounded to the dtype), NEOX RoPE on the first n_rot channels
+    (rounded); causal SDPA of the T queries at positions offset.. over past + new keys (no
+    mask for one token), GQA. Returns (y * sigmoid(gate) [B,T,H*hd], new keys, new values),
+    the new keys/values [B,K,T,hd] as the cache stores them."""
+    B, T, H, two_hd = qg.shape
+    hd = two_hd // 2
+    q, gate = qg[..., :hd], qg[..., hd:]
+    q = rms_norm(q, q_weight, eps).transpose(1, 2)
+    kn = rms_norm(k, k_weight, eps).transpose(1, 2)
+    vn = v.transpose(1, 2)
+    q, kn = apply_rope(q, cos[..., :n_rot], sin[..., :n_rot]), apply_rope(kn, cos[..., :n_rot], sin[..., :n_rot])
+    kk = kn if k_past is None else torch.cat([k_past.to(kn.dtype), kn], 2)
+    vv = vn if v_past is None else torch.cat([v_past.to(vn.dtype), vn], 2)
+    offset = kk.shape[2] - T
+    mask = None if T == 1 else attention_mask(T, kk.shape[2], offset).to(q.device)
+    kw = {"enable_gqa": True} if kk.shape[1] != H else {}
+    y = F.scaled_dot_product_attention(q, kk, vv, attn_mask=mask, **kw)
+    y = y.transpose(1, 2).reshape(B, T, H * hd)
+    return y * torch.sigmoid(gate.reshape(B, T, -1)), kn, vn

@@ -21,15 +21,7 @@ from torch import nn
 
 from .attention import DECODE_MAX_T, _HIP_DTYPES, _HIP_HEAD_DIMS, _hip_ready, hip_disabled
 from .norm import RMSNorm
-
-
-def rope_partial(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_rot: int) -> torch.Tensor:
-    """NEOX RoPE on the first n_rot channels of x [B, H, T, hd] in fp32, rounded to x's dtype;
-    the other channels pass through (qwen35.py:179-184)."""
-    r, rest = x[..., :n_rot].float(), x[..., n_rot:]
-    x1, x2 = r.chunk(2, dim=-1)
-    rot = torch.cat([-x2, x1], dim=-1)
-    return torch.cat([(r * cos + rot * sin).to(x.dtype), rest], dim=-1)
+from .rope import apply_rope
 
 
 class GatedAttention(nn.Module):
@@ -60,7 +52,9 @@ class GatedAttention(nn.Module):
         qv = self.q_norm(qv).transpose(1, 2)
         k = self.k_norm(self.k_proj(x).view(B, T, c.n_kv_heads, c.head_dim)).transpose(1, 2)
         v = self.v_proj(x).view(B, T, c.n_kv_heads, c.head_dim).transpose(1, 2)
-        qv, k = rope_partial(qv, cos, sin, c.n_rot), rope_partial(k, cos, sin, c.n_rot)
+        # NEOX RoPE on the first n_rot channels (tables narrower than the head: partial RoPE)
+        cos, sin = cos[..., :c.n_rot], sin[..., :c.n_rot]
+        qv, k = apply_rope(qv, cos, sin), apply_rope(k, cos, sin)
         if self._use_hip(qv, cache):
             y = self._attend_hip(qv, k, v, cache)          # [B, T, H, hd]
             self.last_path = "hip"

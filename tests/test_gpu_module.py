@@ -329,10 +329,11 @@ def test_fused_qkv_projection_matches_separate():
         assert torch.isfinite(b(x, cos, sin)).all()
 
 
-def _hip_against_cpu(mod, d_model, kv, cos_t, sin_t, seed, expect_hip):
+def _hip_against_cpu(mod, d_model, kv, cos_t, sin_t, seed, expect_hip, oracle_step=None):
     """Runs mod on the GPU (HIP path) and a copy of it on the CPU (the reference's eager
     path, so no reference attention runs on the GPU) over a 40-token prefill and 3 decode
-    steps through a cache; returns [(gpu_out, cpu_out)] per call."""
+    steps through a cache; returns [(gpu_out, cpu_out, oracle_out)] per call, oracle_out
+    from oracle_step(T, pos) (called right after the GPU call) or None."""
     import copy
 
     from sleuth_amd.kv_cache import KVCache
@@ -349,9 +350,10 @@ def _hip_against_cpu(mod, d_model, kv, cos_t, sin_t, seed, expect_hip):
             c, s_ = cos_t[p:p + T], sin_t[p:p + T]
             got = mod(x.to(DEV), c.to(DEV), s_.to(DEV), caches["gpu"]).float().cpu()
             assert mod.last_path == expect_hip(T)
+            want = None if oracle_step is None else oracle_step(T, p).float()
             ref = cpu(x, c, s_, caches["cpu"]).float()
             assert cpu.last_path == "torch"
-            outs.append((got, ref))
+            outs.append((got, ref, want))
             for cache in caches.values():
                 cache.advance(T)
     return outs
@@ -369,31 +371,54 @@ def test_partial_rope_on_the_hip_path(dtype):
     a = Attention(cfg, 0).eval().to(DEV, dtype)
     cos_t, sin_t = oracle.rope_tables(32, 64, 1e4)
     prefill = "hip-prefill" if dtype != torch.float32 else "hip-decode"
-    for got, ref in _hip_against_cpu(a, 256, (2, 64), cos_t, sin_t, 2,
-                                     lambda T: prefill if T > 16 else "hip-decode"):
+    for got, ref, _ in _hip_against_cpu(a, 256, (2, 64), cos_t, sin_t, 2,
+                                        lambda T: prefill if T > 16 else "hip-decode"):
         assert max_abs(got, ref) <= (1e-4 if dtype == torch.float32 else 2e-2)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_gated_attention_hip_matches_torch(dtype):
+def test_gated_attention_hip_matches_oracle(dtype):
     """Qwen3.5 gated attention (qwen35.py:187-216): q/gate split, partial RoPE, sigmoid gate.
-    The kernels' cache write and attention match the reference's eager path (run on the CPU)."""
+    The module on the HIP path (cache write and attention in the kernels) over a 40-token
+    prefill and 3 decode steps, against oracle.gated_attention (pinned by float64 loops) on
+    the module's own projections, and the module's torch path on the CPU."""
     from types import SimpleNamespace
 
     from sleuth_amd.gated import GatedAttention
 
-    cfg = SimpleNamespace(n_heads=4, n_kv_heads=2, head_dim=64, n_rot=32, norm_eps=1e-6)
+    H, K, hd, n_rot, d = 4, 2, 64, 32, 256
+    cfg = SimpleNamespace(n_heads=H, n_kv_heads=K, head_dim=hd, n_rot=n_rot, norm_eps=1e-6)
     torch.manual_seed(3)
     m = GatedAttention(cfg, 0)
-    d = 256
-    m.q_proj = torch.nn.Linear(d, 4 * 2 * 64, bias=False)
-    m.k_proj = torch.nn.Linear(d, 2 * 64, bias=False)
-    m.v_proj = torch.nn.Linear(d, 2 * 64, bias=False)
-    m.o_proj = torch.nn.Linear(4 * 64, d, bias=False)
+    m.q_proj = torch.nn.Linear(d, H * 2 * hd, bias=False)
+    m.k_proj = torch.nn.Linear(d, K * hd, bias=False)
+    m.v_proj = torch.nn.Linear(d, K * hd, bias=False)
+    m.o_proj = torch.nn.Linear(H * hd, d, bias=False)
+    with torch.no_grad():
+        m.q_norm.weight.add_(0.1 * torch.randn(hd))
+        m.k_norm.weight.add_(0.1 * torch.randn(hd))
     m = m.eval().to(DEV, dtype)
-    cos_t, sin_t = oracle.rope_tables(32, 64, 1e6)
-    for got, ref in _hip_against_cpu(m, d, (2, 64), cos_t, sin_t, 4, lambda T: "hip"):
-        assert max_abs(got, ref) <= (1e-4 if dtype == torch.float32 else 2e-2)
+    rec = {}
+    for name in ("q", "k", "v"):
+        getattr(m, f"{name}_proj").register_forward_hook(lambda mod, i, o, n=name: rec.__setitem__(n, o))
+    cos_t, sin_t = oracle.rope_tables(n_rot, 64, 1e6)
+    tol_ = 1e-4 if dtype == torch.float32 else 2e-2
+    past = {}
+
+    def oracle_step(T, p):
+        qg = rec["q"].cpu().view(2, T, H, 2 * hd)
+        k = rec["k"].cpu().view(2, T, K, hd)
+        v = rec["v"].cpu().view(2, T, K, hd)
+        y, kn, vn = oracle.gated_attention(qg, k, v, cos=cos_t[p:p + T], sin=sin_t[p:p + T], n_rot=n_rot,
+                                           q_weight=m.q_norm.weight.cpu(), k_weight=m.k_norm.weight.cpu(),
+                                           eps=1e-6, k_past=past.get("k"), v_past=past.get("v"))
+        past["k"] = kn if "k" not in past else torch.cat([past["k"], kn], 2)
+        past["v"] = vn if "v" not in past else torch.cat([past["v"], vn], 2)
+        return torch.nn.functional.linear(y.float(), m.o_proj.weight.float().cpu())
+
+    for got, ref, want in _hip_against_cpu(m, d, (K, hd), cos_t, sin_t, 4, lambda T: "hip", oracle_step):
+        assert max_abs(got, want) <= tol_
+        assert max_abs(got, ref) <= tol_
 
 
 # ----------------------------------------------------------------------------- host objects
@@ -525,3 +550,67 @@ def test_shared_layers_on_gpu(cuda_graph):
             del os.environ["SLEUTH_AMD_NO_HIP"]
         assert m.blocks[0].attn.last_path == "torch"
         assert (torch_logits - full).abs().max().item() < 0.1
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("sliding", [False, True])
+def test_drafter_attention_module_on_gpu(dtype, sliding):
+    """The drafter's attention module (mtp.py:73-92) on the HIP path, against the oracle
+    (oracle.drafter_attention after the reference's eager norm + RoPE); then its graph form
+    (mtp.py:169-188): n_past held in a device tensor, the call captured once and replayed at
+    two positions, each against the oracle."""
+    from sleuth_amd.drafter import DrafterAttention
+
+    torch.manual_seed(11)
+    H, K, hd, d, L, window = 8, 2, 128, 512, 1200, 512
+    m = DrafterAttention(d, H, hd, sliding=sliding, window=window).eval()
+    with torch.no_grad():
+        m.q_norm.weight.add_(0.1 * torch.randn(hd))
+    m = m.to(DEV, dtype)
+    g = torch.Generator().manual_seed(12)
+    k = torch.randn(1, K, L, hd, generator=g).to(dtype)
+    v = torch.randn(1, K, L, hd, generator=g).to(dtype)
+    cos_t, sin_t = oracle.rope_tables(hd, L + 1, 1e6)
+    kd, vd, cd, sd = k.to(DEV), v.to(DEV), cos_t.to(DEV), sin_t.to(DEV)
+    tol_ = 1e-4 if dtype == torch.float32 else 2e-2
+
+    def want(h, n_past):
+        with torch.no_grad():
+            q = torch.nn.functional.linear(h.cpu().float(), m.q_proj.weight.cpu().float())
+            q = q.to(dtype).view(1, 1, H, hd).transpose(1, 2)
+            qn = oracle.eager_norm_rope(q, m.q_norm.weight.cpu(), m.eps, cos_t[n_past:n_past + 1],
+                                        sin_t[n_past:n_past + 1])
+            y = oracle.drafter_attention(qn.float(), k.float(), v.float(), n_past, window if sliding else 0)
+            return torch.nn.functional.linear(y.transpose(1, 2).reshape(1, 1, H * hd).to(dtype).float(),
+                                              m.o_proj.weight.cpu().float())
+
+    for n_past in (1, 300, 1100):
+        h = torch.randn(1, 1, d, generator=g).to(dtype).to(DEV)
+        with torch.no_grad():
+            got = m(h, kd, vd, cd[n_past:n_past + 1], sd[n_past:n_past + 1], n_past)
+        assert m.last_path == "hip"
+        assert max_abs(got, want(h, n_past)) <= tol_, n_past
+
+    h_buf = torch.zeros(1, 1, d, device=DEV, dtype=dtype)
+    pos = torch.zeros(1, dtype=torch.long, device=DEV)
+
+    def call():
+        return m(h_buf, kd, vd, cd.index_select(0, pos), sd.index_select(0, pos), pos)
+
+    with torch.no_grad():
+        pos.fill_(600)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            call()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = call()
+    for n_past in (700, 1190):
+        h = torch.randn(1, 1, d, generator=g).to(dtype)
+        h_buf.copy_(h)
+        pos.fill_(n_past)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert max_abs(out, want(h_buf, n_past)) <= tol_, n_past

@@ -306,3 +306,68 @@ def test_hip_gate_on_cpu():
     cfg = ModelConfig(vocab_size=10, d_model=64, n_heads=4)
     a = Attention(cfg, 0)
     assert not a._use_hip(torch.zeros(1, 4, 1, 16), None, None)
+
+
+@pytest.mark.parametrize("sliding,n_past", [(False, 1), (False, 40), (True, 5), (True, 40)])
+def test_drafter_attention_module_torch_path(sliding, n_past):
+    """The MTP drafter's attention (mtp.py:73-92) on the CPU: RMSNorm then RoPE at position
+    n_past (two roundings), the target's first n_past keys (sliding: the last window-1), scale
+    1.0, GQA, o_proj -- against the oracle; the device-position form (mtp.py:169-188, n_past
+    as a tensor and a mask over the whole view) gives the same result."""
+    from sleuth_amd.drafter import DrafterAttention
+
+    torch.manual_seed(2)
+    H, K, hd, d, L = 4, 2, 16, 32, 48
+    m = DrafterAttention(d, H, hd, sliding=sliding, window=8).eval()
+    with torch.no_grad():
+        m.q_norm.weight.add_(0.1 * torch.randn(hd))
+    h = torch.randn(2, 1, d)
+    k, v = torch.randn(2, K, L, hd), torch.randn(2, K, L, hd)
+    cos_t, sin_t = oracle.rope_tables(hd, L + 1, 1e4)
+    c, s_ = cos_t[n_past:n_past + 1], sin_t[n_past:n_past + 1]
+    with torch.no_grad():
+        got = m(h, k, v, c, s_, n_past)
+        got_dev = m(h, k, v, c, s_, torch.tensor([n_past]))
+        q = m.q_proj(h).view(2, 1, H, hd).transpose(1, 2)
+        qn = oracle.eager_norm_rope(q, m.q_norm.weight, m.eps, c, s_)
+        y = oracle.drafter_attention(qn, k, v, n_past, 8 if sliding else 0)
+        want = m.o_proj(y.transpose(1, 2).reshape(2, 1, H * hd))
+    assert m.last_path == "torch"
+    torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-4)
+    torch.testing.assert_close(got_dev, want, atol=1e-5, rtol=1e-4)
+
+
+def test_gated_attention_torch_path_matches_oracle():
+    """Qwen3.5 gated attention (qwen35.py:187-216) on the CPU, through a cache (prefill 7,
+    then 2 single tokens), against oracle.gated_attention on the module's own projections."""
+    from types import SimpleNamespace
+
+    from sleuth_amd.gated import GatedAttention
+
+    H, K, hd, n_rot, d = 4, 2, 16, 8, 32
+    cfg = SimpleNamespace(n_heads=H, n_kv_heads=K, head_dim=hd, n_rot=n_rot, norm_eps=1e-6)
+    torch.manual_seed(9)
+    m = GatedAttention(cfg, 0)
+    m.q_proj, m.k_proj = torch.nn.Linear(d, H * 2 * hd, bias=False), torch.nn.Linear(d, K * hd, bias=False)
+    m.v_proj, m.o_proj = torch.nn.Linear(d, K * hd, bias=False), torch.nn.Linear(H * hd, d, bias=False)
+    with torch.no_grad():
+        m.q_norm.weight.add_(0.1 * torch.randn(hd))
+    m.eval()
+    cos_t, sin_t = oracle.rope_tables(n_rot, 16, 1e6)
+    cache = KVCache([(K, hd)], 2, 16, "cpu", torch.float32)
+    kp = vp = None
+    with torch.no_grad():
+        for T in (7, 1, 1):
+            p = cache.pos
+            x = torch.randn(2, T, d)
+            got = m(x, cos_t[p:p + T], sin_t[p:p + T], cache)
+            cache.advance(T)
+            qg = m.q_proj(x).view(2, T, H, 2 * hd)
+            k, v = m.k_proj(x).view(2, T, K, hd), m.v_proj(x).view(2, T, K, hd)
+            y, kn, vn = oracle.gated_attention(qg, k, v, cos=cos_t[p:p + T], sin=sin_t[p:p + T], n_rot=n_rot,
+                                               q_weight=m.q_norm.weight, k_weight=m.k_norm.weight, eps=1e-6,
+                                               k_past=kp, v_past=vp)
+            kp = kn if kp is None else torch.cat([kp, kn], 2)
+            vp = vn if vp is None else torch.cat([vp, vn], 2)
+            torch.testing.assert_close(got, m.o_proj(y), atol=1e-5, rtol=1e-4)
+    assert m.last_path == "torch"

@@ -395,3 +395,70 @@ def test_downstream_argmax_check_has_teeth():
     for name, wrong in planted.items():
         r = downstream_argmax(wrong.transpose(1, 2), ref)
         assert r["mismatched"] > 0, (name, r)
+
+
+def _gated_brute(qg, k, v, cos, sin, n_rot, wq, wk, eps, offset, k_past, v_past):
+    """Qwen3.5 gated attention from its definition in float64 with explicit loops: per head
+    h, q = first half of qg[h], gate = second half; RMSNorm (gain) then rotation of the
+    pairs (i, i + n_rot/2), i < n_rot/2, by angle cos/sin; channels >= n_rot untouched;
+    softmax over keys j <= offset + t with scale hd^-1/2; KV head h // (H/K); times sigmoid(gate)."""
+    B, T, H, two = qg.shape
+    hd, K = two // 2, k.shape[2]
+
+    def norm_rot(x, w, t):
+        x = x.double()
+        x = x / math.sqrt(float((x * x).mean()) + eps) * w.double()
+        out = x.clone()
+        half = n_rot // 2
+        for i in range(half):
+            c, s = float(cos[t, i]), float(sin[t, i])
+            out[i] = x[i] * c - x[i + half] * s
+            out[i + half] = x[i + half] * c + x[i] * s
+        return out
+
+    y = torch.zeros(B, T, H * hd, dtype=torch.float64)
+    for b in range(B):
+        keys = [k_past[b, :, j].double() for j in range(offset)]
+        vals = [v_past[b, :, j].double() for j in range(offset)]
+        for t in range(T):
+            keys.append(torch.stack([norm_rot(k[b, t, kh], wk, t) for kh in range(K)]))
+            vals.append(v[b, t].double())
+        for t in range(T):
+            for h in range(H):
+                kh = h // (H // K)
+                qv = norm_rot(qg[b, t, h, :hd], wq, t)
+                js = range(offset + t + 1)
+                sc = [float((qv * keys[j][kh]).sum()) / math.sqrt(hd) for j in js]
+                mx = max(sc)
+                wts = [math.exp(x - mx) for x in sc]
+                tot = sum(wts)
+                acc = sum(w_ / tot * vals[j][kh] for w_, j in zip(wts, js))
+                gate = qg[b, t, h, hd:].double()
+                y[b, t, h * hd:(h + 1) * hd] = acc / (1 + torch.exp(-gate))
+    return y
+
+
+@pytest.mark.parametrize("T,offset", [(5, 0), (1, 6), (3, 4)])
+def test_gated_attention_pinned_by_float64_loops(T, offset):
+    g = torch.Generator().manual_seed(40 + T)
+    B, H, K, hd, n_rot = 2, 4, 2, 8, 4
+    qg = torch.randn(B, T, H, 2 * hd, generator=g)
+    k, v = torch.randn(B, T, K, hd, generator=g), torch.randn(B, T, K, hd, generator=g)
+    kp, vp = torch.randn(B, K, offset, hd, generator=g), torch.randn(B, K, offset, hd, generator=g)
+    wq, wk = 1 + 0.2 * torch.randn(hd, generator=g), 1 + 0.2 * torch.randn(hd, generator=g)
+    cos_t, sin_t = oracle.rope_tables(n_rot, offset + T, 1e4)
+    c, s = cos_t[offset:], sin_t[offset:]
+    y, kn, vn = oracle.gated_attention(qg, k, v, cos=c, sin=s, n_rot=n_rot, q_weight=wq, k_weight=wk, eps=1e-6,
+                                       k_past=kp if offset else None, v_past=vp if offset else None)
+    want = _gated_brute(qg, k, v, c, s, n_rot, wq, wk, 1e-6, offset, kp, vp)
+    torch.testing.assert_close(y.double(), want, atol=1e-5, rtol=1e-5)
+    assert kn.shape == (B, K, T, hd) and torch.equal(vn, v.transpose(1, 2))
+    # plausible slips the pin catches: q and gate swapped; RoPE over every channel
+    bad = oracle.gated_attention(torch.cat([qg[..., hd:], qg[..., :hd]], -1), k, v, cos=c, sin=s, n_rot=n_rot,
+                                 q_weight=wq, k_weight=wk, eps=1e-6, k_past=kp if offset else None,
+                                 v_past=vp if offset else None)[0]
+    assert not torch.allclose(bad.double(), want, atol=1e-3)
+    c8, s8 = oracle.rope_tables(hd, offset + T, 1e4)
+    bad = oracle.gated_attention(qg, k, v, cos=c8[offset:], sin=s8[offset:], n_rot=hd, q_weight=wq, k_weight=wk,
+                                 eps=1e-6, k_past=kp if offset else None, v_past=vp if offset else None)[0]
+    assert not torch.allclose(bad.double(), want, atol=1e-3)
