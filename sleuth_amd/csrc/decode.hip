@@ -72,6 +72,10 @@ struct SplitParams {
   int64_t sob, sot, soh;
   int persist;    // 1: persistent grid walking the unit list (splitk_kernel)
   int vec_tables; // 1: cos/sin rows and q gains are 16-byte aligned (vector loads)
+  int small_dma;  // 1: q rows and tables may be fetched by 16-byte DMA with 32-bit offsets
+  int span_chunks;  // dense grid of a windowed layer: blockIdx.x counts chunks from the unit's
+                    // first visible one (the grid covers only the chunks a window can touch);
+                    // 0: blockIdx.x is the absolute chunk
   float2* ws_ml;  // [B*H*T][max_chunks] (m, l)
   float* ws_o;    // [B*H*T][max_chunks][D]
   int* ws_ctr;    // work ticket of the persistent grid (zeroed before each launch), or null
@@ -204,7 +208,7 @@ template <int D, int ROWS> struct SplitShared {
 // caller guarantees the block is converged (the unit may leave early, block-uniformly).
 template <typename T, int D, int ROWS>
 __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, const int kvh,
-                                           const int rb, const int c, SplitShared<D, ROWS>& sh,
+                                           const int rb, const int c_in, SplitShared<D, ROWS>& sh,
                                            int* ticket = nullptr) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int LPR = D / VEC;  // lanes per key row
@@ -240,8 +244,9 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
       kmax[r] = -1;
     }
   }
+  const int c = p.span_chunks ? kmin_rb / p.chunk + c_in : c_in;  // absolute chunk
   const int c0 = c * p.chunk;
-  if (c0 > kmax_rb || c0 + p.chunk - 1 < kmin_rb) {  // block-uniform
+  if (c >= p.max_chunks || c0 > kmax_rb || c0 + p.chunk - 1 < kmin_rb) {  // block-uniform
     if (ticket && tid == 0) *ticket = (int)gridDim.x + atomicAdd(p.ws_ctr, 1);
     return;
   }
@@ -636,7 +641,10 @@ template <int D> struct VerifyTile {
   static constexpr int LOADS = TILEB / (WAVES * 1024);
   static constexpr int STAGES = 4;              // LDS stages of K and V: three tiles in flight
   static constexpr int MAX_TOK = ROWS / 4 + 1;  // tokens under one unit's rows (G >= 4)
-  static constexpr int TAB_BYTES = (1 + 2 * MAX_TOK) * D * 4;  // q gains, cos and sin rows
+  // q gains, cos rows and sin rows (fp32), each region padded to whole KB (the DMA unit)
+  static constexpr int TAB_G = (4 * D + 1023) / 1024 * 1024;
+  static constexpr int TAB_R = (MAX_TOK * 4 * D + 1023) / 1024 * 1024;
+  static constexpr int TAB_BYTES = TAB_G + 2 * TAB_R;
   static constexpr int LDS_BYTES = STAGES * 2 * TILEB + TAB_BYTES;
   static constexpr int DW = D / WAVES;          // output channels per wave
   static_assert(LOADS * WAVES * 1024 == TILEB, "tile must split into whole wave loads");
@@ -670,11 +678,8 @@ __device__ __forceinline__ int vswz_v(int row) { return (row & 3) << 2; }
 // Wait until at most N vector-memory loads of this wave are outstanding (they retire in
 // issue order, so everything issued before the last N has landed).
 template <int N> __device__ __forceinline__ void vwait_vm() {
-  static_assert(N == 0 || N == 4 || N == 8 || N == 16, "add the count");
-  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  static_assert(N >= 0 && N <= 63, "vmcnt holds 0..63");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 template <typename T, int D>
@@ -692,7 +697,6 @@ void verify_mfma_kernel(SplitParams p) {
   const int lane = tid % kWave;
   const int n = lane & 31;
   const int hi = lane >> 5;
-  const int c = blockIdx.x;
   const int kvh = blockIdx.y % p.K;
   const int rb = blockIdx.y / p.K;
   const int b = blockIdx.z;
@@ -713,8 +717,9 @@ void verify_mfma_kernel(SplitParams p) {
     visible_range32(base + rb * TL::ROWS / p.G, p.window, (int)p.max_len, umin, dummy);
     visible_range32(base + r_hi / p.G, p.window, (int)p.max_len, dummy, umax);
   }
+  const int c = p.span_chunks ? umin / p.chunk + (int)blockIdx.x : (int)blockIdx.x;  // absolute chunk
   const int c0 = c * p.chunk;
-  if (c0 > umax || c0 + p.chunk - 1 < umin) return;  // block-uniform
+  if (c >= p.max_chunks || c0 > umax || c0 + p.chunk - 1 < umin) return;  // block-uniform
   int t_first = umin > c0 ? (umin - c0) / BN : 0;
   int t_last = (umax - c0) / BN;
   if (t_last > p.chunk / BN - 1) t_last = p.chunk / BN - 1;
@@ -743,22 +748,27 @@ void verify_mfma_kernel(SplitParams p) {
     }
   };
 
-  // ---- prologue: the first STAGES - 1 tiles' loads, this lane's q row, and the block's
-  // q gains and RoPE rows staged in LDS (one memory round trip for all of them; loaded per
-  // lane they took one round trip per 16 channels)
+  // ---- prologue: the unit's q rows, q gains and RoPE rows, and the first STAGES - 1 tiles.
+  // Loads retire in issue order, so the small loads go out FIRST: waiting for them (a
+  // vmcnt of the tile loads issued after them) leaves the tiles streaming while q is
+  // normalised and rotated. With small_dma (aligned tables, offsets within 32 bits) they
+  // are DMA'd straight into LDS: raw q rows into the V slot of the last stage, tables into
+  // `tab`; otherwise they go through registers and wait for the tiles too.
   const bool gains = (p.flags & FORGE_NORM_QK) && p.qw;
   const bool rope = (p.flags & FORGE_ROPE) != 0;
   const int tok_lo = rb * TL::ROWS / p.G;
   const int tok_hi = (rb * TL::ROWS + TL::ROWS - 1 < p.rows_total - 1 ? rb * TL::ROWS + TL::ROWS - 1 : p.rows_total - 1) / p.G;
   const int ntok = tok_hi - tok_lo + 1;  // <= MAX_TOK for G >= 4
-  float* tab = reinterpret_cast<float*>(smem + TL::STAGES * 2 * TL::TILEB);  // [gains | cos tok | sin tok][D]
-#pragma unroll
-  for (int i = 0; i < TL::STAGES - 1; ++i) issue(i);
-  // The q prologue is split over the waves: this lane normalises and rotates row
+  char* tab_b = smem + TL::STAGES * 2 * TL::TILEB;  // [gains | cos rows | sin rows], regions padded
+  float* tab = reinterpret_cast<float*>(tab_b);
+  const float* tab_cos = reinterpret_cast<const float*>(tab_b + TL::TAB_G);
+  const float* tab_sin = reinterpret_cast<const float*>(tab_b + TL::TAB_G + TL::TAB_R);
+  T* qs = reinterpret_cast<T*>(smem + (2 * (TL::STAGES - 1)) * TL::TILEB);        // normalised [ROWS][D]
+  T* qraw = reinterpret_cast<T*>(smem + (2 * (TL::STAGES - 1) + 1) * TL::TILEB);  // raw [ROWS][D]
+  static_assert(TL::ROWS * D * 2 == TL::TILEB, "the raw q rows fill one tile slot");
+  // The q math is split over the waves: this lane normalises and rotates row
   // qr = 8 * wave + lane / 8 of the unit, first-half channels qx .. qx + QCH - 1 and their
-  // RoPE partners qx + D/2. The q values are loaded unconditionally (rows past the end read
-  // row 0 of head kvh * G and are zeroed below): a conditional load made the compiler wait
-  // for it here.
+  // RoPE partners qx + D/2. Rows past the end read row 0 of head kvh * G and are zeroed.
   constexpr int QCH = D / 16;  // first-half channels per lane, 8 lanes per row
   const int qr = 8 * wave + (lane >> 3);
   const int qx = QCH * (lane & 7);
@@ -766,17 +776,70 @@ void verify_mfma_kernel(SplitParams p) {
   const bool qvalid = qflat < p.rows_total;
   const int qtok = qvalid ? qflat / p.G : 0;
   uint4 qa[QCH / 8], qz[QCH / 8];
-  {
-    const int qh = kvh * p.G + (qvalid ? qflat % p.G : 0);
-    const T* src = static_cast<const T*>(p.q) + b * p.sqb + qh * p.sqh + qtok * p.sqt + qx;
+  if (p.small_dma) {
+    // raw q rows: instruction j of this wave fills bytes [(wave * QI + j) KB, +1 KB) of qraw
+    constexpr int QI = TL::TILEB / 1024 / TL::WAVES;
+    const char* qb = static_cast<const char*>(p.q) + (int64_t)b * p.sqb * (int64_t)sizeof(T);
+#pragma unroll
+    for (int j = 0; j < QI; ++j) {
+      const int inst = wave * QI + j;
+      const int off = inst * 1024 + 16 * lane;
+      const int r = off / (2 * D), cb = off % (2 * D);
+      const int fl = rb * TL::ROWS + r;
+      const bool ok = fl < p.rows_total;
+      const int64_t src = ((int64_t)(kvh * p.G + (ok ? fl % p.G : 0)) * p.sqh +
+                           (int64_t)(ok ? fl / p.G : 0) * p.sqt) * (int64_t)sizeof(T) + cb;
+      lds_dma16(qb, (unsigned)src, lds_offset(qraw) + inst * 1024);
+    }
+    // table rows, 1 KB per instruction, instruction i of the block on wave i % WAVES; lanes
+    // past a region's last row re-read its last 16 bytes into the region's padding
+    int inst0 = 0;
+    auto dma_rows = [&](const float* src, int64_t stride, int rows, unsigned dst) {
+      const int bytes = rows * 4 * D;
+      const int ninst = (bytes + 1023) / 1024;
+      for (int i = 0; i < ninst; ++i) {
+        if ((inst0 + i) % TL::WAVES != wave) continue;
+        int off = i * 1024 + 16 * lane;
+        if (off > bytes - 16) off = bytes - 16;
+        const int r = off / (4 * D), cb = off % (4 * D);
+        lds_dma16(src, (unsigned)(r * stride * 4 + cb), dst + i * 1024);
+      }
+      inst0 += ninst;
+    };
+    if (gains) dma_rows(p.qw, 0, 1, lds_offset(tab_b));
+    if (rope) {
+      const int64_t row0 = b * p.csb + (int64_t)tok_lo * p.cst;
+      dma_rows(p.cos + row0, p.cst, ntok, lds_offset(tab_b + TL::TAB_G));
+      dma_rows(p.sin + row0, p.cst, ntok, lds_offset(tab_b + TL::TAB_G + TL::TAB_R));
+    }
+#pragma unroll
+    for (int i = 0; i < TL::STAGES - 1; ++i) issue(i);
+    // this wave's small loads have landed once at most its tile loads remain
+    const int pro_tiles = ntiles < TL::STAGES - 1 ? ntiles : TL::STAGES - 1;
+    static_assert(TL::STAGES - 1 == 3, "one wait per prologue tile count");
+    if (pro_tiles >= 3) vwait_vm<6 * TL::LOADS>();
+    else if (pro_tiles == 2) vwait_vm<4 * TL::LOADS>();
+    else vwait_vm<2 * TL::LOADS>();
+    __syncthreads();  // every wave's q rows and tables are in LDS (tiles may be in flight)
+    const T* qrow = qraw + qr * D + qx;
 #pragma unroll
     for (int j = 0; j < QCH / 8; ++j) {
-      qa[j] = load16(src + 8 * j);
-      qz[j] = load16(src + D / 2 + 8 * j);
+      qa[j] = *reinterpret_cast<const uint4*>(qrow + 8 * j);
+      qz[j] = *reinterpret_cast<const uint4*>(qrow + D / 2 + 8 * j);
     }
-  }
-  {
-    // every value's load goes out before the first store (one round trip, not one per value)
+  } else {
+#pragma unroll
+    for (int i = 0; i < TL::STAGES - 1; ++i) issue(i);
+    {
+      const int qh = kvh * p.G + (qvalid ? qflat % p.G : 0);
+      const T* src = static_cast<const T*>(p.q) + b * p.sqb + qh * p.sqh + qtok * p.sqt + qx;
+#pragma unroll
+      for (int j = 0; j < QCH / 8; ++j) {
+        qa[j] = load16(src + 8 * j);
+        qz[j] = load16(src + D / 2 + 8 * j);
+      }
+    }
+    // every table value's load goes out before the first store (one round trip)
     constexpr int NV = ((1 + 2 * TL::MAX_TOK) * D + TL::WAVES * kWave - 1) / (TL::WAVES * kWave);
     const int nrow = (gains ? 1 : 0) + (rope ? 2 * ntok : 0);
     float v[NV];
@@ -791,24 +854,24 @@ void verify_mfma_kernel(SplitParams p) {
         const int rr = gains ? r : r + 1;  // table row: 0 gains, 1..ntok cos, ntok+1.. sin
         if (rr == 0) {
           v[j] = p.qw[x];
+          dsti[j] = x;
         } else {
-          const int tk = tok_lo + (rr - 1) % ntok;
-          v[j] = (rr <= ntok ? p.cos : p.sin)[b * p.csb + (int64_t)tk * p.cst + x];
+          const int k = (rr - 1) % ntok;
+          v[j] = (rr <= ntok ? p.cos : p.sin)[b * p.csb + (int64_t)(tok_lo + k) * p.cst + x];
+          dsti[j] = (rr <= ntok ? TL::TAB_G : TL::TAB_G + TL::TAB_R) / 4 + k * D + x;
         }
-        dsti[j] = (rr == 0 ? 0 : (rr <= ntok ? rr : rr - ntok + TL::MAX_TOK)) * D + x;
       }
     }
 #pragma unroll
     for (int j = 0; j < NV; ++j)
       if (dsti[j] >= 0) tab[dsti[j]] = v[j];
+    __syncthreads();  // tables in LDS (the tile loads may still be in flight)
   }
-  __syncthreads();  // tables in LDS (the tile loads may still be in flight)
 
   // Fused RMSNorm + RoPE of this lane's q values in fp32, one rounding (as the split
   // kernel's q prologue), staged as T in the K slot of the last stage (not loaded until the
   // loop's first barrier); then every wave reads the Q^T operands of its lane's row n:
   // channels 16s + 8hi + e.
-  T* qs = reinterpret_cast<T*>(smem + (2 * (TL::STAGES - 1)) * TL::TILEB);  // [ROWS][D]
   {
     float a[QCH], z[QCH];
 #pragma unroll
@@ -852,8 +915,8 @@ void verify_mfma_kernel(SplitParams p) {
         }
       }
       if (rope && qvalid) {
-        const float* cr = tab + (1 + (qtok - tok_lo)) * D;
-        const float* sr = tab + (1 + TL::MAX_TOK + (qtok - tok_lo)) * D;
+        const float* cr = tab_cos + (qtok - tok_lo) * D;
+        const float* sr = tab_sin + (qtok - tok_lo) * D;
         float c1[8], s1[8], c2[8], s2[8];
         load_f32x8(cr + x, c1);
         load_f32x8(sr + x, s1);
@@ -1092,6 +1155,18 @@ static int resident_blocks(const void* kernel) {
   return n;
 }
 
+// Dense grid over the chunks of the call: with a window, a unit's rows see at most
+// window + T - 1 keys, so the grid covers that many chunks counted from each unit's first
+// visible one (p.span_chunks) instead of every chunk of max_kv_len.
+static int dense_chunks(SplitParams& p) {
+  p.span_chunks = 0;
+  if (p.window > 0) {
+    const int64_t span = ((int64_t)p.window + p.T - 1 + p.chunk - 1) / p.chunk + 1;
+    if (span < p.max_chunks) p.span_chunks = (int)span;
+  }
+  return p.span_chunks ? p.span_chunks : p.max_chunks;
+}
+
 template <typename T, int D>
 static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
   const int n_rb = (p.rows_total + rows - 1) / rows;
@@ -1124,7 +1199,7 @@ static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
   } else {
     if ((int64_t)p.K * n_rb > 65535 || p.B > 65535) return set_error("grid too large");
     p.persist = 0;
-    grid = dim3((unsigned)p.max_chunks, (unsigned)(p.K * n_rb), (unsigned)p.B);
+    grid = dim3((unsigned)dense_chunks(p), (unsigned)(p.K * n_rb), (unsigned)p.B);
   }
   switch (rows) {
 #define FORGE_ROWS(R) \
@@ -1153,7 +1228,7 @@ static int launch_verify_d(SplitParams p, hipStream_t s) {
   const int n_rb = (p.rows_total + kVerifyRows - 1) / kVerifyRows;
   if ((int64_t)p.K * n_rb > 65535 || p.B > 65535) return set_error("grid too large");
   p.persist = 0;
-  const dim3 grid((unsigned)p.max_chunks, (unsigned)(p.K * n_rb), (unsigned)p.B);
+  const dim3 grid((unsigned)dense_chunks(p), (unsigned)(p.K * n_rb), (unsigned)p.B);
   hipLaunchKernelGGL((verify_mfma_kernel<T, D>), grid, dim3(256), TL::LDS_BYTES, s, p);
   int st = check_launch();
   if (st || p.max_chunks < 2) return st;
@@ -1278,6 +1353,12 @@ int decode_setup(SplitParams& p, int dtype, int B, int T, int H, int K, int D, c
   p.soh = soh;
   p.vec_tables = ((uintptr_t)q_weight | (uintptr_t)cos | (uintptr_t)sin) % 16 == 0 &&
                  (cos == nullptr || (s_cos_b % 4 == 0 && s_cos_t % 4 == 0));
+  // the MFMA verify kernel DMAs q rows (offsets from the batch row's start) and table rows
+  // (from the unit's first token's row) with 32-bit byte offsets
+  const int64_t esize = dtype == FORGE_F32 ? 4 : 2;
+  const int64_t q_span = ((int64_t)(H - 1) * sqh + (int64_t)(T - 1) * sqt + D) * esize;
+  const int64_t tab_span = cos ? ((int64_t)T * s_cos_t + D) * 4 : 0;
+  p.small_dma = p.vec_tables && q_span < (1LL << 31) && tab_span < (1LL << 31);
   return 0;
 }
 
