@@ -56,22 +56,26 @@ __device__ __forceinline__ void store_vec(T* p, const float* in) {
   }
 }
 
-template <typename T, int VEC, int GW>
+// A lane group handles RPL rows: RPL consecutive heads of one (b, t). They share the
+// token's RoPE row and the gain, so those are loaded once per group rather than once per
+// row, and the group has all RPL rows' loads in flight together.
+template <typename T, int VEC, int GW, int RPL>
 __global__ __launch_bounds__(256) void row_norm_rope_kernel(RowParams p) {
-  constexpr int ROWS_PER_BLOCK = 256 / GW;
+  constexpr int GROUPS = 256 / GW;  // lane groups per block
   const int li = threadIdx.x % GW;
-  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + threadIdx.x / GW;
-  const int64_t rows0 = (int64_t)p.B * p.t[0].heads * p.T;
-  const int64_t rows1 = p.ntensors > 1 ? (int64_t)p.B * p.t[1].heads * p.T : 0;
-  if (row >= rows0 + rows1) return;  // whole group leaves together
-  const bool second = row >= rows0;
+  const int64_t grp = (int64_t)blockIdx.x * GROUPS + threadIdx.x / GW;
+  const int64_t groups0 = (int64_t)p.B * p.t[0].heads * p.T / RPL;
+  const int64_t groups1 = p.ntensors > 1 ? (int64_t)p.B * p.t[1].heads * p.T / RPL : 0;
+  if (grp >= groups0 + groups1) return;  // whole group leaves together
+  const bool second = grp >= groups0;
   const RowTensor& rt = second ? p.t[1] : p.t[0];
-  const int64_t r = second ? row - rows0 : row;
-  // heads fastest: the groups of a wave share one token's RoPE row (cache hits), and
-  // read neighbouring heads of the projection (C3 append 29.4 -> 28.7 us)
-  const int h = (int)(r % rt.heads);
-  const int t = (int)((r / rt.heads) % p.T);
-  const int b = (int)(r / ((int64_t)p.T * rt.heads));
+  // rows are ordered (b, t, head) with the head fastest (the groups of a wave read
+  // neighbouring heads of the projection and share one token's RoPE row); the host makes
+  // RPL divide the head count, so a group's rows are heads h0 .. h0 + RPL - 1 of one token
+  const int64_t r0 = (second ? grp - groups0 : grp) * RPL;
+  const int h0 = (int)(r0 % rt.heads);
+  const int t = (int)((r0 / rt.heads) % p.T);
+  const int b = (int)(r0 / ((int64_t)p.T * rt.heads));
 
   const int half = p.D / 2;
   const int c0 = li * VEC;
@@ -83,31 +87,46 @@ __global__ __launch_bounds__(256) void row_norm_rope_kernel(RowParams p) {
     if (drow < 0 || drow >= p.dst_len) return;  // never write past the cache
   }
 
-  const T* src = static_cast<const T*>(rt.src) + b * rt.sb + h * rt.sh + t * rt.st;
-  float a[VEC], z[VEC];
-  if (active) {
-    load_vec<T, VEC>(src + c0, a);
-    load_vec<T, VEC>(src + half + c0, z);
-  } else {
+  const T* src = static_cast<const T*>(rt.src) + b * rt.sb + h0 * rt.sh + t * rt.st;
+  float a[RPL][VEC], z[RPL][VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) a[i] = z[i] = 0.0f;
+  for (int j = 0; j < RPL; ++j) {
+    if (active) {
+      load_vec<T, VEC>(src + j * rt.sh + c0, a[j]);
+      load_vec<T, VEC>(src + j * rt.sh + half + c0, z[j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) a[j][i] = z[j][i] = 0.0f;
+    }
   }
   if (rt.norm) {
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) ss += a[i] * a[i] + z[i] * z[i];
-    ss = group_sum<GW>(ss);
-    const float rs = rsqrtf(ss / (float)p.D + p.eps);
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      a[i] *= rs;
-      z[i] *= rs;
-    }
-    if (rt.w && active) {
+    float wa[VEC], wz[VEC];
+    const bool gain = rt.w && active;
+    if (gain) {
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
-        a[i] *= rt.w[c0 + i];
-        z[i] *= rt.w[half + c0 + i];
+        wa[i] = rt.w[c0 + i];
+        wz[i] = rt.w[half + c0 + i];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < RPL; ++j) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) ss += a[j][i] * a[j][i] + z[j][i] * z[j][i];
+      ss = group_sum<GW>(ss);
+      const float rs = rsqrtf(ss / (float)p.D + p.eps);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        a[j][i] *= rs;
+        z[j][i] *= rs;
+      }
+      if (gain) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          a[j][i] *= wa[i];
+          z[j][i] *= wz[i];
+        }
       }
     }
   }
@@ -115,34 +134,59 @@ __global__ __launch_bounds__(256) void row_norm_rope_kernel(RowParams p) {
   if (rt.rope) {
     const float* cr = p.cos + b * p.csb + t * p.cst;
     const float* sr = p.sin + b * p.csb + t * p.cst;
+    float ca[VEC], sa[VEC], cz[VEC], sz[VEC];
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
-      const float na = a[i] * cr[c0 + i] - z[i] * sr[c0 + i];
-      const float nz = z[i] * cr[half + c0 + i] + a[i] * sr[half + c0 + i];
-      a[i] = na;
-      z[i] = nz;
+      ca[i] = cr[c0 + i];
+      sa[i] = sr[c0 + i];
+      cz[i] = cr[half + c0 + i];
+      sz[i] = sr[half + c0 + i];
     }
+#pragma unroll
+    for (int j = 0; j < RPL; ++j)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float na = a[j][i] * ca[i] - z[j][i] * sa[i];
+        const float nz = z[j][i] * cz[i] + a[j][i] * sz[i];
+        a[j][i] = na;
+        z[j][i] = nz;
+      }
   }
-  T* dst = static_cast<T*>(rt.dst) + b * rt.db + h * rt.dh + drow * rt.dt;
-  store_vec<T, VEC>(dst + c0, a);
-  store_vec<T, VEC>(dst + half + c0, z);
+  T* dst = static_cast<T*>(rt.dst) + b * rt.db + h0 * rt.dh + drow * rt.dt;
+#pragma unroll
+  for (int j = 0; j < RPL; ++j) {
+    store_vec<T, VEC>(dst + j * rt.dh + c0, a[j]);
+    store_vec<T, VEC>(dst + j * rt.dh + half + c0, z[j]);
+  }
 }
 
-template <typename T, int VEC>
-static int launch_rows_vec(const RowParams& p, int gw, hipStream_t s) {
+template <typename T, int VEC, int RPL>
+static int launch_rows_rpl(const RowParams& p, int gw, hipStream_t s) {
   const int64_t rows =
       (int64_t)p.B * p.T * (p.t[0].heads + (p.ntensors > 1 ? p.t[1].heads : 0));
   if (rows == 0) return 0;
-  const int64_t rpb = 256 / gw;
-  const dim3 grid((unsigned)((rows + rpb - 1) / rpb));
+  const int64_t gpb = 256 / gw;
+  const int64_t groups = rows / RPL;
+  const dim3 grid((unsigned)((groups + gpb - 1) / gpb));
   switch (gw) {
 #define FORGE_GW(W) \
-  case W: hipLaunchKernelGGL((row_norm_rope_kernel<T, VEC, W>), grid, dim3(256), 0, s, p); break;
+  case W: hipLaunchKernelGGL((row_norm_rope_kernel<T, VEC, W, RPL>), grid, dim3(256), 0, s, p); break;
     FORGE_GW(1) FORGE_GW(2) FORGE_GW(4) FORGE_GW(8) FORGE_GW(16) FORGE_GW(32) FORGE_GW(64)
 #undef FORGE_GW
     default: return set_error("row kernel: unsupported group width");
   }
   return check_launch();
+}
+
+// Rows per lane group: 4 (or 2) consecutive heads when every tensor's head count allows.
+template <typename T, int VEC>
+static int launch_rows_vec(const RowParams& p, int gw, hipStream_t s) {
+  auto divides = [&](int r) {
+    return p.t[0].heads % r == 0 && (p.ntensors < 2 || p.t[1].heads % r == 0);
+  };
+  if (divides(4)) return launch_rows_rpl<T, VEC, 4>(p, gw, s);
+  if (divides(2)) return launch_rows_rpl<T, VEC, 2>(p, gw, s);
+  return launch_rows_rpl<T, VEC, 1>(p, gw, s);
 }
 
 template <typename T>
