@@ -22,12 +22,16 @@ SOURCES = ["abi.hip", "prep.hip", "decode.hip", "prefill.hip"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU ops (v_pk_*_f32).
+# atomic optimizer off: the kernels' atomics are single-lane work tickets; the optimizer's
+# wave-wide rewrite reads the result at once (a wait for the round trip) where the kernel
+# means to read it much later.
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wno-unused-command-line-argument",
 ]
 

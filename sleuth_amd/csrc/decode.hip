@@ -10,9 +10,10 @@
 // Inside a block, LPR = D / VEC lanes share one key row: each lane loads 16 bytes
 // (VEC elements) of K and of V with one 128-bit load, so a group of LPR lanes reads a
 // whole row. Per iteration, group g takes the NK keys kb0 + u*NG + g (u < NK), so each
-// load instruction of a wave reads 64 / LPR consecutive rows (1 KB for D = 128). The
-// next iteration's K/V loads are issued before the current one is scored (two register
-// buffers), and the first ones before the q prologue, so HBM latency overlaps the math.
+// load instruction of a wave reads 64 / LPR consecutive rows (1 KB for D = 128). A
+// rotating set of register buffers keeps the loads of the next iterations in flight while
+// one is scored, and the q rows are requested before them, so HBM latency overlaps the
+// math.
 // Scores use v_dot2_f32_{bf16,f16} on packed q/k pairs and a DPP butterfly over the LPR
 // lanes; the online softmax keeps a reference max that only moves when a score exceeds
 // it by 2^8 (kRescaleLog2), so the rescale of (l, o) is rare. Groups are then merged
@@ -37,14 +38,14 @@ namespace forge {
 #ifndef FORGE_SPLIT_NK
 #define FORGE_SPLIT_NK 2
 #endif
-#ifndef FORGE_SPLIT_PF
-#define FORGE_SPLIT_PF 3
-#endif
 constexpr int kSplitThreads = 256;
 constexpr int kSplitNK = FORGE_SPLIT_NK;  // keys per group per iteration
-constexpr int kSplitPF = FORGE_SPLIT_PF;  // register buffers: loads run PF - 1 iterations ahead
 constexpr int kMaxChunk = 512;
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale: weights stay <= 2^8
+// Register buffers of the K/V pipeline (loads run PF - 1 iterations ahead): deeper where
+// few query rows leave the registers for it. Measured on C4-shaped ragged decode: PF 4
+// at 3 waves per SIMD streams faster than PF 3 at 4.
+template <int ROWS> constexpr int split_pf() { return ROWS <= 2 ? 4 : 3; }
 
 struct SplitParams {
   const void* q;
@@ -155,44 +156,137 @@ __device__ __forceinline__ uint4 load_nt(const T* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// Loads one q row slice (VEC values at li*VEC), with the optional fused RMSNorm + RoPE,
-// rounded once to T (the dtype the reference's q has when SDPA reads it); returned as
-// the raw 16 bytes (packed pairs for dot2).
-template <typename T, int D, int VEC, int LPR>
-__device__ __forceinline__ uint4 load_q_row(const SplitParams& p, int b, int h, int t, int li) {
-  const T* src = static_cast<const T*>(p.q) + b * p.sqb + h * p.sqh + t * p.sqt + li * VEC;
-  const uint4 raw = load16(src);
-  if (!(p.flags & (FORGE_NORM_QK | FORGE_ROPE))) return raw;
-  float q[VEC];
-  unpack16<T>(raw, q);
-  if (p.flags & FORGE_NORM_QK) {
-    float ss = 0.0f;
+// VEC consecutive fp32 values: 16-byte loads when the caller's tables allow it (a
+// block-uniform flag), else scalar loads of the same values.
+template <int VEC>
+__device__ __forceinline__ void load_f32_row(const float* ptr, float* out, bool vec) {
+  if (vec) {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) ss += q[e] * q[e];
-    ss = group_sum<LPR>(ss);
-    const float rs = rsqrtf(ss / (float)D + p.eps);
+    for (int i = 0; i < VEC; i += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(ptr + i);
+      out[i] = a.x; out[i + 1] = a.y; out[i + 2] = a.z; out[i + 3] = a.w;
+    }
+  } else {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) q[e] *= rs;
-    if (p.qw) {
+    for (int e = 0; e < VEC; ++e) out[e] = ptr[e];
+  }
+}
+
+// Value of lane li ^ (LPR/2) of an aligned LPR-lane group (the NEOX RoPE partner). For
+// 16-lane groups that is a rotation of each DPP row by 8; otherwise a cross-lane shuffle.
+template <int LPR>
+__device__ __forceinline__ float rope_partner(float x) {
+  if constexpr (LPR == 16) {
+    constexpr int kDppRowRor8 = 0x128;
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kDppRowRor8, 0xF, 0xF, false));
+  } else {
+    return __shfl_xor(x, LPR / 2, kWave);
+  }
+}
+
+// The q side of one work unit, in two steps so that its loads go out ahead of the K/V
+// prefetch and their latency overlaps it: fetch() requests the raw 16-byte slice of every
+// row (a row past the end re-reads the last row; its results are never written) and, when the tables
+// are held (TABLES: up to two rows), the gain slice and each row's cos/sin slices;
+// finish() applies the optional fused RMSNorm + RoPE and rounds once to T (the dtype the
+// reference's q has when SDPA reads it), returning the raw 16 bytes (packed pairs for
+// dot2). Without TABLES the table loads happen in finish().
+template <typename T, int D, int ROWS>
+struct QRows {
+  static constexpr int VEC = 16 / sizeof(T);
+  static constexpr int LPR = D / VEC;
+  static constexpr bool TABLES = ROWS <= 2;
+  static constexpr int TW = TABLES ? VEC : 1;
+  uint4 raw[ROWS];
+  float w[TW];
+  float c[TABLES ? ROWS : 1][TW], s[TABLES ? ROWS : 1][TW];
+
+  __device__ __forceinline__ void fetch(const SplitParams& p, int b, int kvh, int rb, int li) {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) q[e] *= p.qw[li * VEC + e];
+    for (int r = 0; r < ROWS; ++r) {
+      int flat = rb * ROWS + r;
+      flat = flat < p.rows_total ? flat : p.rows_total - 1;
+      raw[r] = load16(static_cast<const T*>(p.q) + b * p.sqb + (kvh * p.G + flat % p.G) * p.sqh +
+                      (flat / p.G) * p.sqt + li * VEC);
+    }
+    if constexpr (TABLES) {
+      if ((p.flags & FORGE_NORM_QK) && p.qw) load_f32_row<VEC>(p.qw + li * VEC, w, p.vec_tables);
+      if (p.flags & FORGE_ROPE) {
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+          int flat = rb * ROWS + r;
+          flat = flat < p.rows_total ? flat : p.rows_total - 1;
+          const int64_t off = b * p.csb + (flat / p.G) * p.cst + li * VEC;
+          load_f32_row<VEC>(p.cos + off, c[r], p.vec_tables);
+          load_f32_row<VEC>(p.sin + off, s[r], p.vec_tables);
+        }
+      }
     }
   }
-  if (p.flags & FORGE_ROPE) {
-    // NEOX pairing c <-> c + D/2: the partner slice is in lane li ^ (LPR/2).
-    const float* cr = p.cos + b * p.csb + t * p.cst + li * VEC;
-    const float* sr = p.sin + b * p.csb + t * p.cst + li * VEC;
-    const bool first_half = li < LPR / 2;
-    float y[VEC];
+
+  __device__ __forceinline__ uint4 finish(const SplitParams& p, int b, int rb, int r, int li) const {
+    if (!(p.flags & (FORGE_NORM_QK | FORGE_ROPE))) return raw[r];
+    float q[VEC];
+    unpack16<T>(raw[r], q);
+    const int flat = rb * ROWS + r < p.rows_total ? rb * ROWS + r : p.rows_total - 1;
+    const int t = flat / p.G;
+    if (p.flags & FORGE_NORM_QK) {
+      float ss = 0.0f;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float partner = __shfl_xor(q[e], LPR / 2, kWave);
-      y[e] = first_half ? q[e] * cr[e] - partner * sr[e] : q[e] * cr[e] + partner * sr[e];
+      for (int e = 0; e < VEC; ++e) ss += q[e] * q[e];
+      ss = group_sum<LPR>(ss);
+      const float rs = rsqrtf(ss / (float)D + p.eps);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) q[e] *= rs;
+      if (p.qw) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) q[e] *= TABLES ? w[e % TW] : p.qw[li * VEC + e];
+      }
     }
+    if (p.flags & FORGE_ROPE) {
+      // NEOX pairing c <-> c + D/2: the partner slice is in lane li ^ (LPR/2).
+      const float* cr = p.cos + b * p.csb + t * p.cst + li * VEC;
+      const float* sr = p.sin + b * p.csb + t * p.cst + li * VEC;
+      const bool first_half = li < LPR / 2;
+      float y[VEC];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) q[e] = y[e];
+      for (int e = 0; e < VEC; ++e) {
+        const float partner = rope_partner<LPR>(q[e]);
+        const float ce = TABLES ? c[r % (TABLES ? ROWS : 1)][e % TW] : cr[e];
+        const float se = TABLES ? s[r % (TABLES ? ROWS : 1)][e % TW] : sr[e];
+        y[e] = first_half ? q[e] * ce - partner * se : q[e] * ce + partner * se;
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) q[e] = y[e];
+    }
+    return pack16<T>(q);
   }
-  return pack16<T>(q);
+};
+
+// Buffer resource of one (batch row, KV head) slab of the cache (gfx9 raw buffer: stride
+// 0, range `bytes`). A load at a byte offset >= the range returns zeros without touching
+// memory, which is how the split-K loop skips keys outside a unit's range while still
+// issuing every load (kSkipOffset).
+constexpr unsigned kBufferConfig = 0x00020000u;
+
+// s_waitcnt immediate (gfx9 layout) that waits until at most the K and V loads of `ITERS`
+// prefetched iterations (2 * NK each) are in flight; exp and lgkm counts left at maximum.
+template <int ITERS, int NK> constexpr int kWaitPrefetch() {
+  constexpr int n = 2 * NK * ITERS;
+  static_assert(n < 64, "vmcnt is 6 bits");
+  return (n & 0xF) | (0x7 << 4) | (0xF << 8) | ((n >> 4) << 14);
+}
+constexpr unsigned kSkipOffset = 0x80000000u;  // beyond every slab (host check: < 2^31 bytes)
+constexpr int kNonTemporal = 2;                // cache policy of the streaming loads (nt)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slab_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kBufferConfig);
+}
+
+__device__ __forceinline__ uint4 load_slab(__amdgpu_buffer_rsrc_t rs, unsigned off) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, kNonTemporal));
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 constexpr int kSplitWaves = kSplitThreads / kWave;
@@ -204,12 +298,13 @@ template <int D, int ROWS> struct SplitShared {
   float l[kSplitWaves][ROWS];
 };
 
-// One work unit: rows rb*ROWS .. of KV head kvh of batch row b, keys of chunk c. The
-// caller guarantees the block is converged (the unit may leave early, block-uniformly).
+// One work unit: rows rb*ROWS .. of KV head kvh of batch row b (whose first new token
+// sits at position `base`), keys of chunk c. The caller guarantees the block is converged
+// (the unit may leave early, block-uniformly) and passes block-uniform arguments.
 template <typename T, int D, int ROWS>
-__device__ __forceinline__ void split_unit(const SplitParams& p, const int b, const int kvh,
-                                           const int rb, const int c_in, SplitShared<D, ROWS>& sh,
-                                           int* ticket = nullptr) {
+__device__ __forceinline__ void split_unit(const SplitParams& p, const int b, const int base,
+                                           const int kvh, const int rb, const int c_in,
+                                           SplitShared<D, ROWS>& sh, int* ticket = nullptr) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int LPR = D / VEC;  // lanes per key row
   static_assert(LPR >= 2 && LPR <= kWave && (LPR & (LPR - 1)) == 0, "bad head dim");
@@ -222,9 +317,6 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
   const int li = tid % LPR;
   const int g = tid / LPR;
   const int wave = tid / kWave;
-
-  // Positions fit in 32 bits (host check: max_len < 2^31).
-  const int base = (int)row_base(p.row_pos, p.pos_dev, p.pos0, b);
 
   // Rows of this block and their visible key ranges; the union [kmin_rb, kmax_rb] and
   // the intersection [lo_all, hi_all] over the valid rows.
@@ -247,7 +339,7 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
   const int c = p.span_chunks ? kmin_rb / p.chunk + c_in : c_in;  // absolute chunk
   const int c0 = c * p.chunk;
   if (c >= p.max_chunks || c0 > kmax_rb || c0 + p.chunk - 1 < kmin_rb) {  // block-uniform
-    if (ticket && tid == 0) *ticket = (int)gridDim.x + atomicAdd(p.ws_ctr, 1);
+    if (ticket && tid == 0) *ticket = atomicAdd(p.ws_ctr, 1);
     return;
   }
   const int iters = p.chunk / KPI;
@@ -255,47 +347,54 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
   int it_last = (kmax_rb - c0) / KPI;
   if (it_last > iters - 1) it_last = iters - 1;
 
-  // One (b, kv head) slab of the cache; offsets inside it fit in 32 bits (host check).
-  const T* kbase = static_cast<const T*>(p.kc) + b * p.skb + kvh * p.skh + li * VEC;
-  const T* vbase = static_cast<const T*>(p.vc) + b * p.skb + kvh * p.skh + li * VEC;
-  const int sks = (int)p.sks;
+  // the persistent grid's next work ticket (the counter's old value; the caller adds the
+  // grid size): nothing reads it before the unit's merge, so its round trip hides under
+  // the unit
+  if (ticket && tid == 0) *ticket = atomicAdd(p.ws_ctr, 1);
 
-  // Loads of iteration `it`; keys outside [kmin_rb, kmax_rb] are not read.
+  QRows<T, D, ROWS> qr;
+  qr.fetch(p, b, kvh, rb, li);
+
+  // One (b, kv head) slab of the cache as a buffer; byte offsets inside it fit in 31 bits
+  // (host check), so kSkipOffset lies beyond it.
+  const int64_t slab = b * p.skb + kvh * p.skh;
+  const unsigned row_bytes = (unsigned)p.sks * (unsigned)sizeof(T);
+  const unsigned slab_bytes = (unsigned)(p.max_len - 1) * row_bytes + (unsigned)(D * sizeof(T));
+  const __amdgpu_buffer_rsrc_t krs = slab_rsrc(static_cast<const T*>(p.kc) + slab, slab_bytes);
+  const __amdgpu_buffer_rsrc_t vrs = slab_rsrc(static_cast<const T*>(p.vc) + slab, slab_bytes);
+  const unsigned lane_bytes = (unsigned)(li * VEC * sizeof(T));
+
+  // Loads of iteration `it`. Every load is issued, whatever the branch: keys outside
+  // [kmin_rb, kmax_rb] and the iterations past it_last (the pipeline's tail, never
+  // computed) read zeros through kSkipOffset, without memory traffic. With no load behind
+  // a branch the compiler counts the loads in flight exactly, and an iteration waits only
+  // for its own data, not for the prefetch issued just before it.
   auto load_iter = [&](int it, uint4* kr, uint4* vr) {
     const int kb0 = c0 + it * KPI;
-    const bool inside = kb0 >= kmin_rb && kb0 + KPI - 1 <= kmax_rb;
+    const bool live = it <= it_last;
 #pragma unroll
     for (int u = 0; u < NK; ++u) {
       const int kp = kb0 + u * NG + g;
-      if (inside || (kp >= kmin_rb && kp <= kmax_rb)) {
-        kr[u] = load_nt(kbase + kp * sks);
-        vr[u] = load_nt(vbase + kp * sks);
-      } else {
-        kr[u] = make_uint4(0, 0, 0, 0);
-        vr[u] = make_uint4(0, 0, 0, 0);
-      }
+      const bool in = live && kp >= kmin_rb && kp <= kmax_rb;
+      const unsigned off = in ? (unsigned)kp * row_bytes + lane_bytes : kSkipOffset;
+      kr[u] = load_slab(krs, off);
+      vr[u] = load_slab(vrs, off);
     }
   };
 
-  constexpr int PF = kSplitPF;
+  constexpr int PF = split_pf<ROWS>();
   uint4 kbuf[PF][NK], vbuf[PF][NK];
 #pragma unroll
-  for (int j = 0; j < PF - 1; ++j)
-    if (it_first + j <= it_last) load_iter(it_first + j, kbuf[j], vbuf[j]);
+  for (int j = 0; j < PF; ++j) load_iter(it_first + j, kbuf[j], vbuf[j]);
 
-  // the persistent grid's next work ticket: its round trip hides under this unit
-  if (ticket && tid == 0) *ticket = (int)gridDim.x + atomicAdd(p.ws_ctr, 1);
-
+  // (A row past the end holds a copy of the last row; its results are never written.)
   uint4 q[ROWS];
 #pragma unroll
-  for (int r = 0; r < ROWS; ++r) {
-    const int flat = rb * ROWS + r;
-    if (flat < p.rows_total) {
-      q[r] = load_q_row<T, D, VEC, LPR>(p, b, kvh * p.G + flat % p.G, flat / p.G, li);
-    } else {
-      q[r] = make_uint4(0, 0, 0, 0);
-    }
-  }
+  for (int r = 0; r < ROWS; ++r) q[r] = qr.finish(p, b, rb, r, li);
+  // Everything but the prefetch has landed. Said explicitly so that the compiler's count
+  // of loads in flight at the loop head does not include q/table loads that only some
+  // (flag-dependent) paths consumed; otherwise it waits for every load there.
+  __builtin_amdgcn_s_waitcnt(kWaitPrefetch<PF, NK>());
 
   float m[ROWS], l[ROWS], o[ROWS][VEC];
 #pragma unroll
@@ -357,17 +456,26 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
     }
   };
 
-  // Rotating register pipeline: iteration it reads buffer (it - it_first) % PF and the
-  // loads of iteration it + PF - 1 are issued just before it is computed.
-  for (int it = it_first; it <= it_last; it += PF) {
+  // Rotating register pipeline: iteration it reads buffer (it - it_first) % PF, which is
+  // refilled with iteration it + PF right after, so PF - 1 iterations are in flight while
+  // one is computed. Whole rounds of PF iterations run without an exit in between (an exit
+  // that rejoins the loop's latch would make the compiler wait for every load at the loop
+  // head); the last < PF iterations, already requested, follow.
+  const int n_it = it_last - it_first + 1;
+  const int it_tail = it_first + n_it / PF * PF;
+  for (int it = it_first; it < it_tail; it += PF) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      const int cur = it + j;
-      if (cur > it_last) break;
-      if (cur + PF - 1 <= it_last) load_iter(cur + PF - 1, kbuf[(j + PF - 1) % PF], vbuf[(j + PF - 1) % PF]);
-      compute_iter(cur, kbuf[j], vbuf[j]);
+      compute_iter(it + j, kbuf[j], vbuf[j]);
+      // The refill stays below the compute, so the buffer keeps its registers across the
+      // loop (no copies at the latch, which would wait for every load in flight).
+      __builtin_amdgcn_sched_barrier(0);
+      load_iter(it + j + PF, kbuf[j], vbuf[j]);
     }
   }
+#pragma unroll
+  for (int j = 0; j < PF - 1; ++j)
+    if (it_tail + j <= it_last) compute_iter(it_tail + j, kbuf[j], vbuf[j]);
 
   // Merge the groups of this wave: butterfly over lane distances LPR .. 32.
 #pragma unroll
@@ -437,10 +545,9 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
 }
 
 // Split-K kernel. Persistent mode (p.persist, used when positions come from device
-// memory): a fixed grid of about as many blocks as
-// the GPU holds at once; every block derives the per-row chunk ranges from the device
-// positions (so the launch needs no host knowledge of ragged lengths and stays
-// graph-safe), builds the prefix sum of work units per batch row in LDS, and takes units
+// memory): a fixed grid of kPersistBlocksPerCU blocks per CU; every block derives the
+// per-row chunk ranges from the device positions (so the launch needs no host knowledge
+// of ragged lengths and stays graph-safe), builds the prefix sum of work units per batch row in LDS, and takes units
 // by ticket from a counter in the workspace (zeroed by a one-thread kernel launched just
 // before): blocks on CUs that stream faster take more units, so all blocks finish
 // together. Units are ordered (row b, KV head x row block, chunk) with the chunk fastest,
@@ -452,18 +559,20 @@ constexpr int kPersistMaxRows = 2048;
 
 // Occupancy target: more waves hide more HBM latency, fewer leave registers for the
 // accumulators of ROWS query rows.
-template <int ROWS> constexpr int split_waves_per_eu() { return ROWS <= 2 ? 4 : ROWS == 4 ? 3 : 2; }
+template <int ROWS> constexpr int split_waves_per_eu() { return ROWS <= 4 ? 3 : 2; }
 
 template <typename T, int D, int ROWS>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(split_waves_per_eu<ROWS>())))
 void splitk_kernel(SplitParams p) {
   __shared__ SplitShared<D, ROWS> sh;
   if (!p.persist) {
-    split_unit<T, D, ROWS>(p, blockIdx.z, blockIdx.y % p.K, blockIdx.y / p.K, blockIdx.x, sh);
+    // Positions fit in 32 bits (host check: max_len < 2^30).
+    const int base = (int)row_base(p.row_pos, p.pos_dev, p.pos0, blockIdx.z);
+    split_unit<T, D, ROWS>(p, blockIdx.z, base, blockIdx.y % p.K, blockIdx.y / p.K, blockIdx.x, sh);
     return;
   }
   __shared__ int sh_pref[kPersistMaxRows + 1];
-  __shared__ int sh_cmin[kPersistMaxRows];
+  __shared__ int sh_base[kPersistMaxRows];  // first new token's position of each row
   __shared__ int sh_nch[kPersistMaxRows];
   const int tid = threadIdx.x;
   const int n_rb = (p.rows_total + ROWS - 1) / ROWS;
@@ -471,13 +580,13 @@ void splitk_kernel(SplitParams p) {
   // chunk range of each batch row: union of its T queries' visible keys
   for (int b = tid; b < p.B; b += kSplitThreads) {
     const int base = (int)row_base(p.row_pos, p.pos_dev, p.pos0, b);
+    sh_base[b] = base;
     int lo, hi0, lo1, hi;
     visible_range32(base, p.window, (int)p.max_len, lo, hi0);
     visible_range32(base + p.T - 1, p.window, (int)p.max_len, lo1, hi);
     const int cmin = lo / p.chunk;
     int cmax = hi / p.chunk;
     if (cmax > p.max_chunks - 1) cmax = p.max_chunks - 1;
-    sh_cmin[b] = cmin;
     sh_nch[b] = (hi >= lo && cmax >= cmin) ? cmax - cmin + 1 : 0;
   }
   __syncthreads();
@@ -513,19 +622,25 @@ void splitk_kernel(SplitParams p) {
   // at the end of every iteration keeps the waves within one iteration of each other.
   __shared__ int sh_ticket[2];
   int parity = 0;
-  for (int u = blockIdx.x; u < total; u = sh_ticket[parity], parity ^= 1) {
-    int next = total;
+  // (LDS values are block-uniform; readfirstlane lets the compiler keep the unit's
+  // coordinates, and the cache slab's buffer descriptors built from them, in scalar
+  // registers.)
+  for (int u = blockIdx.x; u < total; u = __builtin_amdgcn_readfirstlane(sh_ticket[parity]), parity ^= 1) {
+    int next = 0;              // split_unit sets it on every path
     int lo = 0, hi = p.B - 1;  // last row with sh_pref[row] <= u
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (sh_pref[mid] <= u) lo = mid;
+      if (__builtin_amdgcn_readfirstlane(sh_pref[mid]) <= u) lo = mid;
       else hi = mid - 1;
     }
-    const int o = u - sh_pref[lo];
-    const int n = sh_nch[lo];
+    const int o = u - __builtin_amdgcn_readfirstlane(sh_pref[lo]);
+    const int n = __builtin_amdgcn_readfirstlane(sh_nch[lo]);
     const int pr = o / n;
-    split_unit<T, D, ROWS>(p, lo, pr % p.K, pr / p.K, sh_cmin[lo] + o % n, sh, &next);
-    if (tid == 0) sh_ticket[parity] = next;
+    const int base = __builtin_amdgcn_readfirstlane(sh_base[lo]);
+    int kmin, kmax;
+    visible_range32(base, p.window, (int)p.max_len, kmin, kmax);  // the row's first chunk
+    split_unit<T, D, ROWS>(p, lo, base, pr % p.K, pr / p.K, kmin / p.chunk + o % n, sh, &next);
+    if (tid == 0) sh_ticket[parity] = (int)gridDim.x + next;
     __syncthreads();  // the next unit reuses the merge LDS; the ticket is visible
   }
 }
@@ -1135,8 +1250,13 @@ static int auto_chunk(int dtype, int B, int /*T*/, int H, int K, int D, int64_t 
   return chunk;
 }
 
-// Blocks of `kernel` the current device holds at once (CUs x occupancy), cached per
-// (device, kernel); host queries only, so the launch stays graph-capturable.
+// Persistent split-K blocks per CU. Fewer concurrent streams read HBM faster: on C4-shaped
+// ragged decode 2 blocks per CU (each with a deeper prefetch) beat filling the CU.
+constexpr int kPersistBlocksPerCU = 2;
+
+// Persistent blocks of `kernel` for the current device: CUs x min(occupancy,
+// kPersistBlocksPerCU), cached per (device, kernel); host queries only, so the launch stays
+// graph-capturable.
 static int resident_blocks(const void* kernel) {
   struct Entry { int dev; const void* k; int n; };
   static Entry cache[64];
@@ -1150,6 +1270,7 @@ static int resident_blocks(const void* kernel) {
   int ncu = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kSplitThreads, 0) != hipSuccess) return 0;
+  if (per_cu > kPersistBlocksPerCU) per_cu = kPersistBlocksPerCU;
   const int n = ncu * (per_cu > 0 ? per_cu : 1);
   if (used < 64) cache[used++] = Entry{dev, kernel, n};
   return n;
@@ -1304,8 +1425,9 @@ int decode_setup(SplitParams& p, int dtype, int B, int T, int H, int K, int D, c
   if ((sqb | sqh | sqt | skb | skh | sks) % vec)
     return set_error("forge_attn_decode: q/cache strides must be multiples of 16 bytes");
   if (max_len <= 0 || max_len >= (1LL << 30)) return set_error("cache length must be in [1, 2^30)");
-  if (sks * (max_len + 1) >= (1LL << 31))
-    return set_error("forge_attn_decode: one (batch, kv head) slab of the cache must hold < 2^31 elements");
+  const int64_t esize = dtype == FORGE_F32 ? 4 : 2;
+  if (sks * (max_len + 1) * esize >= (1LL << 31))
+    return set_error("forge_attn_decode: one (batch, kv head) slab of the cache must span < 2^31 bytes");
   if (max_kv_len <= 0 || max_kv_len > max_len) max_kv_len = max_len;
   if (!row_pos && !pos_dev && (pos0 < 0 || pos0 + T > max_len))
     return set_error("KV cache full: pos + T exceeds the cache length");
@@ -1355,7 +1477,6 @@ int decode_setup(SplitParams& p, int dtype, int B, int T, int H, int K, int D, c
                  (cos == nullptr || (s_cos_b % 4 == 0 && s_cos_t % 4 == 0));
   // the MFMA verify kernel DMAs q rows (offsets from the batch row's start) and table rows
   // (from the unit's first token's row) with 32-bit byte offsets
-  const int64_t esize = dtype == FORGE_F32 ? 4 : 2;
   const int64_t q_span = ((int64_t)(H - 1) * sqh + (int64_t)(T - 1) * sqt + D) * esize;
   const int64_t tab_span = cos ? ((int64_t)T * s_cos_t + D) * 4 : 0;
   p.small_dma = p.vec_tables && q_span < (1LL << 31) && tab_span < (1LL << 31);
