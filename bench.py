@@ -584,7 +584,9 @@ def run_only(args, dev) -> int:
         pf = PrefillWorkload(4, 4096, 16, 8, 128, 1e6, torch.bfloat16, dev)
         warm(pf.step)
         t = time_loop(pf.step, args.steps, args.warmup)
-        print(json.dumps({"workload": "C3 prefill step", "us": round(t * 1e6, 2)}), flush=True)
+        ta = time_loop(pf.attend, args.steps, args.warmup)
+        print(json.dumps({"workload": "C3 prefill step", "us": round(t * 1e6, 2), "attention_us": round(ta * 1e6, 2),
+                          "attention_tflops": round(pf.flops() / ta / 1e12, 1)}), flush=True)
     elif args.only == "extra":
         print(json.dumps(extra_configs(dev, args)), flush=True)
     elif args.only == "sdpa":
