@@ -30,7 +30,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, TFLOP/s
 N_LAYERS = 28                # Qwen3-0.6B: tokens/s counts 28 layers per token
-PREFILL_WARM_S = 0.1         # untimed back-to-back calls before an MFMA-bound timing
+WARM_S = 0.1                 # untimed back-to-back calls before each headline timing
 METRIC = "decode attn HBM GB/s + tokens/s (bs64, 32k ctx); prefill bf16 TFLOPS at 4k"
 
 
@@ -185,10 +185,11 @@ def time_loop(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(stop) / 1e3 / steps
 
 
-def warm(fn, seconds: float = PREFILL_WARM_S) -> int:
-    """Runs fn back to back for about `seconds` of GPU time before a timing: an MFMA-heavy
-    kernel only reaches its steady clock after some tens of milliseconds of load (C3 prefill
-    on MI355X: about 355 us per call in the first 20 calls, 290 us from about the 60th on).
+def warm(fn, seconds: float = WARM_S) -> int:
+    """Runs fn back to back for about `seconds` of GPU time before a timing: the GPU only
+    reaches its steady clock after some tens of milliseconds of load (C3 prefill on MI355X:
+    about 355 us per call in the first 20 calls, 290 us from about the 60th on; the C4
+    attention call: 642 us over its first 20 calls, 615 us over the next 20).
     Returns the number of calls made."""
     calls = 0
     t0 = time.perf_counter()
@@ -396,6 +397,7 @@ def main() -> int:
     wl.append()  # write the new tokens once so the rows are complete before timing
     torch.cuda.synchronize()
     print(f"[bench] C4 decode: B=64, sum L = {sum(lens)}, chunk {wl.chunk}", file=sys.stderr, flush=True)
+    warm(wl.step)
     t_step = time_loop(wl.step, args.steps, args.warmup)
     t_attn = time_loop(wl.attend, args.steps, args.warmup)
     step_gbs = wl.step_bytes() / t_step / 1e9
@@ -448,7 +450,7 @@ def main() -> int:
         # the whole prefill step (forge_kv_append of the 4 x 4096 keys and values, then the
         # attention kernel) against the same causal FLOP count
         "prefill_step_tflops": round(p_step_tflops, 1),
-        "prefill_warm_s": PREFILL_WARM_S,
+        "warm_s": WARM_S,
         "prefill_config": "C3: 4 x 4096 causal, 16 q / 8 kv heads, head dim 128, bf16, QK-norm, RoPE theta 1e6",
         # the reference's own GPU attention call (torch SDPA, flash / memory-efficient backends)
         # on the same GPU and the C3 shapes, attention only
@@ -577,6 +579,7 @@ def run_only(args, dev) -> int:
     if args.only == "decode":
         wl = DecodeWorkload(c4_lengths(args.seed), 16, 8, 128, 1e6, torch.bfloat16, dev, seed=args.seed)
         wl.append()
+        warm(wl.step)
         t = time_loop(wl.step, args.steps, args.warmup)
         print(json.dumps({"workload": "C4 decode step", "us": round(t * 1e6, 2),
                           "GBs": round(wl.step_bytes() / t / 1e9, 1)}), flush=True)
