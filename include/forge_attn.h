@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define FORGE_ABI_VERSION 1
+#define FORGE_ABI_VERSION 2
 
 /* dtype codes */
 #define FORGE_F32 0
@@ -110,6 +110,30 @@ int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, const void* 
                       float scale, int chunk, void* out, int64_t sob, int64_t sot, int64_t soh,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * forge_kv_append followed by forge_attn_decode, in one launch where the shape allows:
+ * the new tokens' raw keys k and values v [B,K,T,D] (strides sknb.., svnb..) are
+ * normalised/rotated (kv_flags: FORGE_NORM_QK with gain k_weight and FORGE_ROPE for the
+ * keys, FORGE_NORM_V for the values; the same cos/sin rows as q), written into the caches
+ * at base_b + t (KVCache.update, kv_cache.py:52-60; StaticKVCache.update 107-114), and
+ * attended to: the split-K unit whose chunk holds a new position makes that key and value
+ * itself and uses them in place of the cache row. The keys, values and outputs are those of
+ * the two calls, bit for bit. Where a lane group would hold more than two new keys, and on
+ * the wide-group MFMA path (G >= 4, bf16/fp16, D 128/256), it issues forge_kv_append's
+ * kernel first. Other arguments and the workspace as forge_attn_decode.
+ */
+int forge_attn_decode_append(int dtype, int B, int T, int H, int K, int D, const void* q,
+                             int64_t sqb, int64_t sqh, int64_t sqt, const float* q_weight,
+                             float eps, int flags, const void* k, int64_t sknb, int64_t sknh,
+                             int64_t sknt, const void* v, int64_t svnb, int64_t svnh,
+                             int64_t svnt, const float* k_weight, int kv_flags,
+                             const float* cos, const float* sin, int64_t s_cos_b,
+                             int64_t s_cos_t, void* k_cache, void* v_cache, int64_t skb,
+                             int64_t skh, int64_t sks, int64_t max_len, const int32_t* row_pos,
+                             const int64_t* pos_dev, int64_t pos0, int64_t max_kv_len,
+                             int window, float scale, int chunk, void* out, int64_t sob,
+                             int64_t sot, int64_t soh, void* workspace, size_t workspace_bytes,
+                             void* stream);
 /*
  * Allocation-free forge_attn_decode (no counterpart in the reference). For callers that
  * cannot allocate device memory: code under graph capture that may not call hipMalloc,

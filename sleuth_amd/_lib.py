@@ -12,7 +12,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libforge_attn.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, BF16, F16 = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 48 * 1024 * 1024   # FORGE_NOALLOC_SCRATCH_BYTES
@@ -46,6 +46,20 @@ SIGNATURES: dict[str, tuple] = {
         _i, _i, _i, _i, _i, _i,              # dtype, B, T, H, K, D
         _p, _i64, _i64, _i64,                # q + strides
         _p, _f, _i,                          # q_weight, eps, flags
+        _p, _p, _i64, _i64,                  # cos, sin, s_cos_b, s_cos_t
+        _p, _p, _i64, _i64, _i64, _i64,      # k_cache, v_cache, skb, skh, sks, max_len
+        _p, _p, _i64, _i64,                  # row_pos, pos_dev, pos0, max_kv_len
+        _i, _f, _i,                          # window, scale, chunk
+        _p, _i64, _i64, _i64,                # out + strides (b, t, h)
+        _p, C.c_size_t,                      # workspace, bytes
+        _p]),
+    "forge_attn_decode_append": (_i, [
+        _i, _i, _i, _i, _i, _i,              # dtype, B, T, H, K, D
+        _p, _i64, _i64, _i64,                # q + strides
+        _p, _f, _i,                          # q_weight, eps, flags
+        _p, _i64, _i64, _i64,                # new k + strides
+        _p, _i64, _i64, _i64,                # new v + strides
+        _p, _i,                              # k_weight, kv_flags
         _p, _p, _i64, _i64,                  # cos, sin, s_cos_b, s_cos_t
         _p, _p, _i64, _i64, _i64, _i64,      # k_cache, v_cache, skb, skh, sks, max_len
         _p, _p, _i64, _i64,                  # row_pos, pos_dev, pos0, max_kv_len

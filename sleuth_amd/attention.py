@@ -9,14 +9,14 @@ Paths (the reference's own dispatch, attention.py:109-153, with the HIP kernels 
 of head_norm_rope + cache.update + SDPA):
   * HIP (GPU inference: no grad, dtype fp32/bf16/fp16, head dim 32/64/128/256, no
     document mask, nobody listening on attn.pattern):
-      forge_kv_append   k norm + RoPE (+ v norm), written into the cache at pos /
-                        pos_t / per-row lengths (with partial RoPE, norm and RoPE run in
-                        torch as the reference's eager code does, and the kernels take
-                        q and k as they are);
-      T <= 16           forge_attn_decode (split-K; decode, verify, static steps), q norm
-                        + RoPE fused into its q load;
-      T > 16            forge_attn_prefill (bf16/fp16 MFMA flash, head dim 64/128/256)
-                        else forge_attn_decode (fp32 and other head sizes).
+      k norm + RoPE (+ v norm), written into the cache at pos / pos_t / per-row
+      lengths (with partial RoPE, norm and RoPE run in torch as the reference's eager
+      code does, and the kernels take q and k as they are), then attention:
+      T > 16, bf16/fp16, head dim 64/128/256: forge_kv_append, then forge_attn_prefill
+                        (MFMA flash) with the q norm + RoPE in its q load;
+      otherwise         forge_attn_decode_append: the cache write and the split-K
+                        attention (decode, verify, static steps, fp32, other head sizes)
+                        in one launch, the q norm + RoPE fused into the q load.
     The output comes back as [B, T, H, hd], the layout o_proj reads.
   * torch (CPU, training, document masks, the pattern tap, or
     SLEUTH_AMD_NO_HIP=1): the reference's eager code, unchanged in meaning.
@@ -238,7 +238,6 @@ class Attention(nn.Module):
         if cache is None:
             kc = torch.empty(B, self.n_kv, T, hd, device=q.device, dtype=q.dtype)
             vc = torch.empty_like(kc)
-            ops.kv_append(k, v, kc, vc, pos=0, norm_v=norm_v, **k_args)
             pos_kw, max_kv, offset, chunk = dict(pos=0), T, 0, 0
         else:
             kc, vc = cache.k[self.layer_idx], cache.v[self.layer_idx]
@@ -257,15 +256,18 @@ class Attention(nn.Module):
                     pos_kw, max_kv, offset = dict(row_pos=rows), top + T, None
                 else:
                     pos_kw, max_kv, offset = dict(pos=cache.pos), cache.pos + T, cache.pos
-            ops.kv_append(k, v, kc, vc, norm_v=norm_v, **pos_kw, **k_args)
 
         if T > DECODE_MAX_T and offset is not None and ops.prefill_supported(q) and \
                 (q_args["cos"] is None or q_args["cos"].dim() == 2):
+            ops.kv_append(k, v, kc, vc, norm_v=norm_v, **pos_kw, **k_args)
             self.last_path = "hip-prefill"
             return ops.attn_prefill(q, kc, vc, scale=self.scale, offset=offset, window=self.window, **q_args)
+        # the cache write and the attention in one call (one launch where the shape allows);
+        # q and k share the RoPE tables and the eps (both come from this module's config)
         self.last_path = "hip-decode"
-        return ops.attn_decode(q, kc, vc, scale=self.scale, max_kv_len=max_kv, window=self.window,
-                               chunk=chunk, **pos_kw, **q_args)
+        return ops.attn_decode_append(q, k, v, kc, vc, scale=self.scale, max_kv_len=max_kv, window=self.window,
+                                      chunk=chunk, norm_v=norm_v, k_weight=k_args.get("k_weight"),
+                                      norm_k=k_args["norm_k"], **pos_kw, **q_args)
 
     # ------------------------------------------------------------------ torch path
     def _forward_torch(self, q, k, v, cos, sin, cache, same_doc) -> torch.Tensor:

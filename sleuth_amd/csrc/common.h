@@ -38,6 +38,14 @@ __device__ __forceinline__ uint4 pack16(const float* in) {
   return raw;
 }
 
+// Marks x as computed: the compiler may then not fold the fp32 operation that produced it
+// into the rounding to a 16-bit type (a v_fma_mix*_f16 rounds once, where the reference's
+// fp32 math followed by .to(dtype) rounds twice).
+__device__ __forceinline__ float fp32_result(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 __device__ __forceinline__ uint4 load16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }

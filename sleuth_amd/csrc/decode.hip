@@ -46,6 +46,9 @@ constexpr float kRescaleLog2 = 8.0f;  // lazy rescale: weights stay <= 2^8
 // few query rows leave the registers for it. Measured on C4-shaped ragged decode: PF 4
 // at 3 waves per SIMD streams faster than PF 3 at 4.
 template <int ROWS> constexpr int split_pf() { return ROWS <= 2 ? 4 : 3; }
+// New positions one lane group may hold in a call of forge_attn_decode_append (T up to
+// kNewPerLane key groups of the block; the host checks it).
+constexpr int kNewPerLane = 2;
 
 struct SplitParams {
   const void* q;
@@ -80,6 +83,16 @@ struct SplitParams {
   float2* ws_ml;  // [B*H*T][max_chunks] (m, l)
   float* ws_o;    // [B*H*T][max_chunks][D]
   int* ws_ctr;    // work ticket of the persistent grid (zeroed before each launch), or null
+  // The new tokens' raw keys and values (forge_attn_decode_append), or null: the unit whose
+  // chunk holds a new position makes that key (norm + RoPE) and value (norm) itself, uses
+  // them in place of the cache rows, and in row block 0 writes them into the cache.
+  const void* kn;
+  const void* vn;
+  int64_t sknb, sknh, sknt, svnb, svnh, svnt;
+  const float* kw;  // gain of the key norm, or null
+  int kvflags;      // FORGE_NORM_QK / FORGE_ROPE for the keys, FORGE_NORM_V for the values
+  void* kcw;        // the caches, written
+  void* vcw;
 };
 
 // Eight fp32 values: two 16-byte loads when the caller's tables allow it (a block-uniform
@@ -263,6 +276,56 @@ struct QRows {
   }
 };
 
+// One lane's 16-byte slice of a new key or value row (the group of LPR lanes holds the
+// row), normalised (gain w, if any) and rotated like forge_kv_append's row kernel: the
+// per-lane sum runs over the pairs (c, c + D/2) in the same order, the group sum over the
+// same lane pattern, the fmas are the same explicit ones and nothing else is contracted,
+// so the two produce the same bits. Every lane of the group must take part (cross-lane
+// steps).
+template <typename T, int D>
+__device__ __forceinline__ uint4 new_row_slice(uint4 raw, bool norm, const float* w, float eps,
+                                               const float* cr, const float* sr, int li) {
+#pragma clang fp contract(off)
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int LPR = D / VEC;
+  if (!norm && !cr) return raw;
+  float x[VEC];
+  unpack16<T>(raw, x);
+  const bool first_half = li < LPR / 2;
+  if (norm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float o = rope_partner<LPR>(x[e]);
+      const float a = first_half ? x[e] : o, z = first_half ? o : x[e];
+      ss += fmaf(a, a, z * z);
+    }
+    ss = group_sum<LPR / 2>(ss);
+    const float rs = rsqrtf(fmaf(ss, 1.0f / (float)D, eps));
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) x[e] *= rs;
+    if (w) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[e] *= w[li * VEC + e];
+    }
+  }
+  if (cr) {
+    float y[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float o = rope_partner<LPR>(x[e]);
+      const float ce = cr[li * VEC + e], se = sr[li * VEC + e];
+      y[e] = first_half ? fmaf(x[e], ce, -(o * se)) : fmaf(x[e], ce, o * se);
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) y[e] = fp32_result(y[e]);
+    return pack16<T>(y);
+  }
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) x[e] = fp32_result(x[e]);
+  return pack16<T>(x);
+}
+
 // Buffer resource of one (batch row, KV head) slab of the cache (gfx9 raw buffer: stride
 // 0, range `bytes`). A load at a byte offset >= the range returns zeros without touching
 // memory, which is how the split-K loop skips keys outside a unit's range while still
@@ -343,6 +406,47 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
     return;
   }
   const int iters = p.chunk / KPI;
+
+  // New positions in this chunk (forge_attn_decode_append): [n_lo, n_hi], block-uniform.
+  // Group g holds the keys c0 + g (mod NG), so at most kNewPerLane of them (host check).
+  int n_lo = 1, n_hi = 0;
+  if (p.kn) {
+    n_lo = base > c0 ? base : c0;
+    n_hi = base + p.T - 1 < c0 + p.chunk - 1 ? base + p.T - 1 : c0 + p.chunk - 1;
+    if (n_hi > (int)p.max_len - 1) n_hi = (int)p.max_len - 1;
+  }
+  const bool has_new = n_lo <= n_hi;
+  int new_pos[kNewPerLane] = {};
+  uint4 new_k[kNewPerLane], new_v[kNewPerLane];
+  if (has_new) {
+    // first position >= n_lo held by this group
+    const int first = n_lo + (((g - (n_lo - c0)) % NG) + NG) % NG;
+#pragma unroll
+    for (int j = 0; j < kNewPerLane; ++j) {
+      const int pp = first + j * NG;
+      new_pos[j] = pp <= n_hi ? pp : -1;
+      const int t = (pp <= n_hi ? pp : n_hi) - base;  // a row of the call, for every lane
+      const T* kr = static_cast<const T*>(p.kn) + b * p.sknb + kvh * p.sknh + t * p.sknt + li * VEC;
+      const T* vr = static_cast<const T*>(p.vn) + b * p.svnb + kvh * p.svnh + t * p.svnt + li * VEC;
+      const bool rope = p.kvflags & FORGE_ROPE;
+      const float* cr = rope ? p.cos + b * p.csb + t * p.cst : nullptr;
+      const float* sr = rope ? p.sin + b * p.csb + t * p.cst : nullptr;
+      new_k[j] = new_row_slice<T, D>(load16(kr), p.kvflags & FORGE_NORM_QK, p.kw, p.eps, cr, sr, li);
+      new_v[j] = new_row_slice<T, D>(load16(vr), p.kvflags & FORGE_NORM_V, nullptr, p.eps, nullptr,
+                                     nullptr, li);
+    }
+    // Each cache row is written by one unit: the one of its chunk whose row block holds
+    // the first query row of the token at that position. That unit always runs, since a
+    // token sees its own key (other row blocks may see nothing in this chunk and leave).
+    const int64_t slab = b * p.skb + kvh * p.skh;
+#pragma unroll
+    for (int j = 0; j < kNewPerLane; ++j)
+      if (new_pos[j] >= 0 && (new_pos[j] - base) * p.G / ROWS == rb) {
+        store16(static_cast<T*>(p.kcw) + slab + (int64_t)new_pos[j] * p.sks + li * VEC, new_k[j]);
+        store16(static_cast<T*>(p.vcw) + slab + (int64_t)new_pos[j] * p.sks + li * VEC, new_v[j]);
+      }
+  }
+
   int it_first = kmin_rb > c0 ? (kmin_rb - c0) / KPI : 0;
   int it_last = (kmax_rb - c0) / KPI;
   if (it_last > iters - 1) it_last = iters - 1;
@@ -405,9 +509,26 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
     for (int e = 0; e < VEC; ++e) o[r][e] = 0.0f;
   }
 
-  auto compute_iter = [&](int it, const uint4* kr, const uint4* vr) {
+  auto compute_iter = [&](int it, const uint4* kin, const uint4* vin) {
     const int kb0 = c0 + it * KPI;
     const bool full = kb0 >= lo_all && kb0 + KPI - 1 <= hi_all;  // every row sees every key
+    uint4 kr[NK], vr[NK];
+#pragma unroll
+    for (int u = 0; u < NK; ++u) {
+      kr[u] = kin[u];
+      vr[u] = vin[u];
+    }
+    if (has_new && kb0 <= n_hi && kb0 + KPI - 1 >= n_lo) {  // block-uniform
+      // the new keys and values stand in for the cache rows, which hold older data
+#pragma unroll
+      for (int u = 0; u < NK; ++u)
+#pragma unroll
+        for (int j = 0; j < kNewPerLane; ++j)
+          if (kb0 + u * NG + g == new_pos[j]) {
+            kr[u] = new_k[j];
+            vr[u] = new_v[j];
+          }
+    }
     float s[ROWS][NK];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
@@ -1530,6 +1651,56 @@ extern "C" int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, c
   if (st) return st;
   const size_t need = decode_need(p, D);
   if (need && (!workspace || workspace_bytes < need)) return set_error("workspace too small");
+  decode_bind(p, D, workspace);
+  return decode_launch(p, dtype, D, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------- decode with the cache write
+extern "C" int forge_attn_decode_append(
+    int dtype, int B, int T, int H, int K, int D, const void* q, int64_t sqb, int64_t sqh,
+    int64_t sqt, const float* q_weight, float eps, int flags, const void* k, int64_t sknb,
+    int64_t sknh, int64_t sknt, const void* v, int64_t svnb, int64_t svnh, int64_t svnt,
+    const float* k_weight, int kv_flags, const float* cos, const float* sin, int64_t s_cos_b,
+    int64_t s_cos_t, void* k_cache, void* v_cache, int64_t skb, int64_t skh, int64_t sks,
+    int64_t max_len, const int32_t* row_pos, const int64_t* pos_dev, int64_t pos0,
+    int64_t max_kv_len, int window, float scale, int chunk, void* out, int64_t sob, int64_t sot,
+    int64_t soh, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  SplitParams p;
+  int st = decode_setup(p, dtype, B, T, H, K, D, q, sqb, sqh, sqt, q_weight, eps, flags, cos, sin,
+                        s_cos_b, s_cos_t, k_cache, v_cache, skb, skh, sks, max_len, row_pos,
+                        pos_dev, pos0, max_kv_len, window, scale, chunk, out, sob, sot, soh);
+  if (st) return st;
+  if (!k || !v) return set_error("forge_attn_decode_append: null k or v");
+  if ((kv_flags & FORGE_ROPE) && (!cos || !sin)) return set_error("FORGE_ROPE needs cos and sin");
+  const int vec = vec_of(dtype);
+  const size_t need = decode_need(p, D);
+  if (need && (!workspace || workspace_bytes < need)) return set_error("workspace too small");
+  // In the split-K kernel when a lane group holds at most kNewPerLane new keys and the rows
+  // allow 16-byte slices; otherwise (the MFMA path among them) forge_kv_append runs first.
+  const int groups = kSplitThreads / (D / vec);
+  const bool fused = !use_verify_mfma(dtype, D, p.G) && T <= kNewPerLane * groups &&
+                     ((uintptr_t)k | (uintptr_t)v | (uintptr_t)k_weight | (uintptr_t)cos | (uintptr_t)sin) % 16 == 0 &&
+                     (sknb | sknh | sknt | svnb | svnh | svnt) % vec == 0;
+  if (!fused) {
+    st = forge_kv_append(dtype, B, T, K, D, k, sknb, sknh, sknt, v, svnb, svnh, svnt, k_cache, v_cache,
+                         skb, skh, sks, max_len, row_pos, pos_dev, pos0, k_weight, eps, kv_flags, cos,
+                         sin, s_cos_b, s_cos_t, stream);
+    if (st) return st;
+  } else {
+    p.kn = k;
+    p.vn = v;
+    p.sknb = sknb;
+    p.sknh = sknh;
+    p.sknt = sknt;
+    p.svnb = svnb;
+    p.svnh = svnh;
+    p.svnt = svnt;
+    p.kw = k_weight;
+    p.kvflags = kv_flags;
+    p.kcw = k_cache;
+    p.vcw = v_cache;
+  }
   decode_bind(p, D, workspace);
   return decode_launch(p, dtype, D, (hipStream_t)stream);
 }

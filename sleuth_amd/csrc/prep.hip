@@ -61,6 +61,10 @@ __device__ __forceinline__ void store_vec(T* p, const float* in) {
 // row, and the group has all RPL rows' loads in flight together.
 template <typename T, int VEC, int GW, int RPL>
 __global__ __launch_bounds__(256) void row_norm_rope_kernel(RowParams p) {
+  // No implicit contraction (fmas are written out, and a product is not folded into its
+  // rounding to fp16): forge_attn_decode_append makes the same rows with the same
+  // operations in its own lane layout and must produce the same bits.
+#pragma clang fp contract(off)
   constexpr int GROUPS = 256 / GW;  // lane groups per block
   const int li = threadIdx.x % GW;
   const int64_t grp = (int64_t)blockIdx.x * GROUPS + threadIdx.x / GW;
@@ -113,9 +117,9 @@ __global__ __launch_bounds__(256) void row_norm_rope_kernel(RowParams p) {
     for (int j = 0; j < RPL; ++j) {
       float ss = 0.0f;
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) ss += a[j][i] * a[j][i] + z[j][i] * z[j][i];
+      for (int i = 0; i < VEC; ++i) ss += fmaf(a[j][i], a[j][i], z[j][i] * z[j][i]);
       ss = group_sum<GW>(ss);
-      const float rs = rsqrtf(ss / (float)p.D + p.eps);
+      const float rs = rsqrtf(fmaf(ss, 1.0f / (float)p.D, p.eps));
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
         a[j][i] *= rs;
@@ -146,8 +150,8 @@ __global__ __launch_bounds__(256) void row_norm_rope_kernel(RowParams p) {
     for (int j = 0; j < RPL; ++j)
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
-        const float na = a[j][i] * ca[i] - z[j][i] * sa[i];
-        const float nz = z[j][i] * cz[i] + a[j][i] * sz[i];
+        const float na = fmaf(a[j][i], ca[i], -(z[j][i] * sa[i]));
+        const float nz = fmaf(z[j][i], cz[i], a[j][i] * sz[i]);
         a[j][i] = na;
         z[j][i] = nz;
       }
@@ -155,6 +159,13 @@ __global__ __launch_bounds__(256) void row_norm_rope_kernel(RowParams p) {
   T* dst = static_cast<T*>(rt.dst) + b * rt.db + h0 * rt.dh + drow * rt.dt;
 #pragma unroll
   for (int j = 0; j < RPL; ++j) {
+    if constexpr (sizeof(T) < 4) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        a[j][i] = fp32_result(a[j][i]);
+        z[j][i] = fp32_result(z[j][i]);
+      }
+    }
     store_vec<T, VEC>(dst + j * rt.dh + c0, a[j]);
     store_vec<T, VEC>(dst + j * rt.dh + half + c0, z[j]);
   }

@@ -231,6 +231,47 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *
     return out
 
 
+def attn_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                       v_cache: torch.Tensor, *, scale: float, pos: int | None = None,
+                       pos_dev: torch.Tensor | None = None, row_pos: torch.Tensor | None = None,
+                       max_kv_len: int | None = None, window: int = 0,
+                       q_weight: torch.Tensor | None = None, k_weight: torch.Tensor | None = None,
+                       eps: float = 1e-6, norm_q: bool = False, norm_k: bool = False,
+                       norm_v: bool = False, cos: torch.Tensor | None = None,
+                       sin: torch.Tensor | None = None, chunk: int = 0, out: torch.Tensor | None = None,
+                       workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """kv_append(k, v, ...) then attn_decode(q, ...), as one forge_attn_decode_append call:
+    the new keys (norm_k with k_weight, RoPE) and values (norm_v) go into the cache at
+    base_b + t and the T queries attend over it, the new keys included. Returns [B,T,H,D]."""
+    B, K, T, D = k.shape
+    if v.shape != k.shape or q.shape[0] != B or q.shape[2] != T or q.shape[3] != D:
+        raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)} and v {tuple(v.shape)} do not fit")
+    if k_cache.shape[1] != K:
+        raise ValueError(f"cache {tuple(k_cache.shape)} does not fit new k {tuple(k.shape)}")
+    if k.dtype != k_cache.dtype:
+        k = k.to(k_cache.dtype)
+    if v.dtype != k_cache.dtype:
+        v = v.to(k_cache.dtype)
+    _need_device(k, v)
+    _last_dim_contiguous(k, "k")
+    _last_dim_contiguous(v, "v")
+    args, out, dev, max_kv_len, chunk = _decode_args(q, k_cache, v_cache, scale, pos, pos_dev, row_pos,
+                                                     max_kv_len, window, q_weight, eps, norm_q, cos, sin,
+                                                     chunk, out, workspace)
+    c = args[13]
+    kv_flags = (NORM_QK if norm_k else 0) | (ROPE if c is not None else 0) | (NORM_V if norm_v else 0)
+    kw = _weight(k_weight, D) if norm_k else None
+    need = lib().forge_attn_decode_workspace_bytes(args[0], B, T, q.shape[1], K, D, max_kv_len, chunk)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    st = lib().forge_attn_decode_append(*args[:13], _ptr(k), k.stride(0), k.stride(1), k.stride(2),
+                                        _ptr(v), v.stride(0), v.stride(1), v.stride(2), _ptr(kw), kv_flags,
+                                        *args[13:], _ptr(workspace), ws_bytes, _stream(dev))
+    check(st, "forge_attn_decode_append")
+    return out
+
+
 def attn_decode_noalloc(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *, scale: float,
                         out: torch.Tensor, pos: int | None = None, pos_dev: torch.Tensor | None = None,
                         row_pos: torch.Tensor | None = None, max_kv_len: int | None = None,
@@ -317,5 +358,5 @@ def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: fl
     return out
 
 
-__all__ = ["head_norm_rope", "kv_append", "attn_decode", "attn_decode_noalloc", "attn_prefill", "decode_chunk",
+__all__ = ["head_norm_rope", "kv_append", "attn_decode", "attn_decode_append", "attn_decode_noalloc", "attn_prefill", "decode_chunk",
            "decode_workspace_bytes", "attn_drafter", "prefill_supported", "dtype_code", "_lib"]

@@ -23,14 +23,14 @@ def declared() -> set[str]:
 
 def test_library_loads_with_abi_version():
     lib = _lib.lib()
-    assert lib.forge_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.forge_abi_version() == _lib.ABI_VERSION == 2
     assert lib.forge_last_error() == b""
 
 
 def test_every_declared_symbol_is_exported_and_bound():
     names = declared()
     assert {"forge_abi_version", "forge_last_error", "forge_head_norm_rope", "forge_kv_append",
-            "forge_attn_decode", "forge_attn_decode_chunk", "forge_attn_decode_workspace_bytes",
+            "forge_attn_decode", "forge_attn_decode_append", "forge_attn_decode_chunk", "forge_attn_decode_workspace_bytes",
             "forge_attn_prefill"} <= names
     raw = C.CDLL(str(_lib.LIB_PATH))
     for n in names:

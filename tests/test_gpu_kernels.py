@@ -310,3 +310,99 @@ def test_prefill_rejects_fp32():
     q = torch.zeros(1, 2, 4, 128, device=DEV)
     with pytest.raises(ValueError):
         ops().attn_prefill(q, q[:, :1], q[:, :1], scale=1.0)
+
+
+# ------------------------------------------------------------------ decode with the cache write
+def _append_decode_pair(seed, dtype, B, H, K, D, T, lens, window, where, norm_v=False, chunk=0,
+                        theta=1e6, max_len=None):
+    """One step twice on one cache: forge_kv_append then forge_attn_decode, and
+    forge_attn_decode_append. lens[b] = keys row b holds after the step (its T new ones
+    included); earlier positions hold N(0,1), later ones 1e4 poison. `where` picks the
+    position source: 'pos' (host, lens equal), 'row_pos' (device, per row), 'pos_dev'."""
+    g = gen(seed)
+    max_len = max_len or max(lens) + 9
+    qkv = randn(g, B, T, H + 2 * K, D, dtype=dtype).to(DEV)
+    q = qkv[:, :, :H].transpose(1, 2)
+    k = qkv[:, :, H:H + K].transpose(1, 2)
+    v = qkv[:, :, H + K:].transpose(1, 2)
+    wq = (1 + 0.1 * randn(g, D)).float().to(DEV)
+    wk = (1 + 0.1 * randn(g, D)).float().to(DEV)
+    base = [L - T for L in lens]
+    cos_t, sin_t = tables(D, max_len + T, theta)
+    c = torch.stack([cos_t[p:p + T] for p in base]).to(DEV)
+    s = torch.stack([sin_t[p:p + T] for p in base]).to(DEV)
+    kc = torch.full((B, K, max_len, D), 1e4, dtype=dtype)
+    vc = torch.full((B, K, max_len, D), 1e4, dtype=dtype)
+    for b, p in enumerate(base):
+        kc[b, :, :p] = randn(g, K, p, D, dtype=dtype)
+        vc[b, :, :p] = randn(g, K, p, D, dtype=dtype)
+    kc, vc = kc.to(DEV), vc.to(DEV)
+    mk = dict(max_kv_len=max_len)
+    if where == "pos":
+        assert len(set(base)) == 1
+        pk, mk = dict(pos=base[0]), {}
+        c, s = c[0], s[0]
+    elif where == "row_pos":
+        pk = dict(row_pos=torch.tensor(base, dtype=torch.int32, device=DEV))
+    else:
+        assert len(set(base)) == 1
+        pk = dict(pos_dev=torch.tensor([base[0]], dtype=torch.int64, device=DEV))
+        c, s = c[0], s[0]
+    qa = dict(scale=scale_of(D), window=window, q_weight=wq, eps=1e-6, norm_q=True, cos=c, sin=s,
+              chunk=chunk, **mk)
+    o = ops()
+    k1, v1 = kc.clone(), vc.clone()
+    o.kv_append(k, v, k1, v1, k_weight=wk, eps=1e-6, norm_k=True, norm_v=norm_v, cos=c, sin=s, **pk)
+    y1 = o.attn_decode(q, k1, v1, **pk, **qa)
+    k2, v2 = kc.clone(), vc.clone()
+    y2 = o.attn_decode_append(q, k, v, k2, v2, k_weight=wk, norm_k=True, norm_v=norm_v, **pk, **qa)
+    torch.cuda.synchronize()
+    return (y1, k1, v1), (y2, k2, v2), (q, k, v, wq, wk, c, s)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("HK", [(8, 4), (12, 4), (16, 8), (8, 1)])
+def test_decode_append_equals_append_then_decode(dtype, D, HK):
+    """forge_attn_decode_append == forge_kv_append + forge_attn_decode bit for bit: the
+    outputs and the whole caches (the rows before, the new ones, the poisoned rest). One
+    new token on ragged rows (persistent grid), through the fused kernel or, for the
+    wide-group MFMA path (G = 8 at bf16/fp16 hd 128/256), the two launches."""
+    H, K = HK
+    a, b, _ = _append_decode_pair(D + H + K, dtype, 4, H, K, D, 1, [1, 18, 300, 777], 0, "row_pos")
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("T", [2, 5, 16])
+@pytest.mark.parametrize("window", [0, 40])
+@pytest.mark.parametrize("where", ["pos", "row_pos", "pos_dev"])
+def test_decode_append_verify_steps(T, window, where):
+    """Verify steps of T new tokens (the new keys may straddle a chunk boundary: 64-key
+    chunks, the new keys at 510 .. 510 + T - 1), host, per-row and device positions, and
+    a values norm: equal to the two calls bit for bit."""
+    lens = [510 + T] * 3 if where != "row_pos" else [T, 510 + T, 900]
+    for dtype, D, (H, K) in ((torch.bfloat16, 128, (16, 8)), (torch.float32, 64, (12, 4)),
+                             (torch.float16, 256, (4, 2))):
+        a, b, _ = _append_decode_pair(T + window, dtype, 3, H, K, D, T, lens, window, where,
+                                      norm_v=(T == 5), chunk=64 if D < 256 else 128)
+        for x, y in zip(a, b):
+            assert torch.equal(x, y), (dtype, D)
+
+
+def test_decode_append_against_the_oracle():
+    """The fused step against the oracle: the keys the reference's KVCache.update would
+    store after head_norm_rope (kv_cache.py:52-60, fused_ops.py:101-121), the values as
+    given, and the attention output of the new token over the whole row."""
+    B, H, K, D, T = 3, 16, 8, 128, 1
+    lens = [40, 1000, 3000]
+    _, (y, kc, vc), (q, k, v, wq, wk, c, s) = _append_decode_pair(77, torch.bfloat16, B, H, K, D, T, lens, 0,
+                                                                  "row_pos")
+    kn = oracle.head_norm_rope(k.cpu(), wk.cpu(), 1e-6, c.cpu(), s.cpu())
+    qn = oracle.head_norm_rope(q.cpu(), wq.cpu(), 1e-6, c.cpu(), s.cpu())
+    for b, L in enumerate(lens):
+        assert max_abs(kc[b, :, L - 1:L], kn[b]) <= 2e-2
+        assert torch.equal(vc[b, :, L - 1:L].cpu(), v[b].cpu())
+        assert (kc[b, :, L:].cpu() == 1e4).all() and (vc[b, :, L:].cpu() == 1e4).all()
+    ref = oracle.ragged_decode(qn.float(), kc.float().cpu(), vc.float().cpu(), lens, 0, scale_of(D))
+    assert max_abs(y, ref.transpose(1, 2)) <= 2e-2
