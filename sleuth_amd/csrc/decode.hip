@@ -47,7 +47,7 @@ constexpr float kRescaleLog2 = 8.0f;  // lazy rescale: weights stay <= 2^8
 // at 3 waves per SIMD streams faster than PF 3 at 4.
 template <int ROWS> constexpr int split_pf() { return ROWS <= 2 ? 4 : 3; }
 // New positions one lane group may hold in a call of forge_attn_decode_append (T up to
-// kNewPerLane key groups of the block; the host checks it).
+// kNewPerLane times the key groups of the block; the host checks it).
 constexpr int kNewPerLane = 2;
 
 struct SplitParams {
@@ -84,8 +84,8 @@ struct SplitParams {
   float* ws_o;    // [B*H*T][max_chunks][D]
   int* ws_ctr;    // work ticket of the persistent grid (zeroed before each launch), or null
   // The new tokens' raw keys and values (forge_attn_decode_append), or null: the unit whose
-  // chunk holds a new position makes that key (norm + RoPE) and value (norm) itself, uses
-  // them in place of the cache rows, and in row block 0 writes them into the cache.
+  // chunk holds a new position makes that key (norm + RoPE) and value (norm), writes them
+  // into the cache and then streams its chunk (one row block per KV head: the only reader).
   const void* kn;
   const void* vn;
   int64_t sknb, sknh, sknt, svnb, svnh, svnt;
@@ -408,43 +408,39 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
   const int iters = p.chunk / KPI;
 
   // New positions in this chunk (forge_attn_decode_append): [n_lo, n_hi], block-uniform.
-  // Group g holds the keys c0 + g (mod NG), so at most kNewPerLane of them (host check).
-  int n_lo = 1, n_hi = 0;
+  // The host takes this path only when one row block covers all of a KV head's query rows,
+  // so this unit is the only one of the launch that reads these cache rows. It makes them
+  // and writes them before its loads: lane group g handles the keys c0 + g (mod NG), both
+  // here and in the stream below, so every lane later loads exactly the 16 bytes it stored
+  // (a thread reads its own earlier write), and nothing extra stays live in the loop.
   if (p.kn) {
-    n_lo = base > c0 ? base : c0;
-    n_hi = base + p.T - 1 < c0 + p.chunk - 1 ? base + p.T - 1 : c0 + p.chunk - 1;
+    int n_lo = base > c0 ? base : c0;
+    int n_hi = base + p.T - 1 < c0 + p.chunk - 1 ? base + p.T - 1 : c0 + p.chunk - 1;
     if (n_hi > (int)p.max_len - 1) n_hi = (int)p.max_len - 1;
-  }
-  const bool has_new = n_lo <= n_hi;
-  int new_pos[kNewPerLane] = {};
-  uint4 new_k[kNewPerLane], new_v[kNewPerLane];
-  if (has_new) {
-    // first position >= n_lo held by this group
-    const int first = n_lo + (((g - (n_lo - c0)) % NG) + NG) % NG;
+    if (n_lo <= n_hi) {  // block-uniform
+      const int first = n_lo + (((g - (n_lo - c0)) % NG) + NG) % NG;  // this group's first
+      const int64_t slab = b * p.skb + kvh * p.skh;
 #pragma unroll
-    for (int j = 0; j < kNewPerLane; ++j) {
-      const int pp = first + j * NG;
-      new_pos[j] = pp <= n_hi ? pp : -1;
-      const int t = (pp <= n_hi ? pp : n_hi) - base;  // a row of the call, for every lane
-      const T* kr = static_cast<const T*>(p.kn) + b * p.sknb + kvh * p.sknh + t * p.sknt + li * VEC;
-      const T* vr = static_cast<const T*>(p.vn) + b * p.svnb + kvh * p.svnh + t * p.svnt + li * VEC;
-      const bool rope = p.kvflags & FORGE_ROPE;
-      const float* cr = rope ? p.cos + b * p.csb + t * p.cst : nullptr;
-      const float* sr = rope ? p.sin + b * p.csb + t * p.cst : nullptr;
-      new_k[j] = new_row_slice<T, D>(load16(kr), p.kvflags & FORGE_NORM_QK, p.kw, p.eps, cr, sr, li);
-      new_v[j] = new_row_slice<T, D>(load16(vr), p.kvflags & FORGE_NORM_V, nullptr, p.eps, nullptr,
-                                     nullptr, li);
-    }
-    // Each cache row is written by one unit: the one of its chunk whose row block holds
-    // the first query row of the token at that position. That unit always runs, since a
-    // token sees its own key (other row blocks may see nothing in this chunk and leave).
-    const int64_t slab = b * p.skb + kvh * p.skh;
-#pragma unroll
-    for (int j = 0; j < kNewPerLane; ++j)
-      if (new_pos[j] >= 0 && (new_pos[j] - base) * p.G / ROWS == rb) {
-        store16(static_cast<T*>(p.kcw) + slab + (int64_t)new_pos[j] * p.sks + li * VEC, new_k[j]);
-        store16(static_cast<T*>(p.vcw) + slab + (int64_t)new_pos[j] * p.sks + li * VEC, new_v[j]);
+      for (int j = 0; j < kNewPerLane; ++j) {
+        const int pp = first + j * NG;
+        const int t = (pp <= n_hi ? pp : n_hi) - base;  // a row of the call, for every lane
+        const T* kr = static_cast<const T*>(p.kn) + b * p.sknb + kvh * p.sknh + t * p.sknt + li * VEC;
+        const T* vr = static_cast<const T*>(p.vn) + b * p.svnb + kvh * p.svnh + t * p.svnt + li * VEC;
+        const bool rope = p.kvflags & FORGE_ROPE;
+        const float* cr = rope ? p.cos + b * p.csb + t * p.cst : nullptr;
+        const float* sr = rope ? p.sin + b * p.csb + t * p.cst : nullptr;
+        const uint4 nk = new_row_slice<T, D>(load16(kr), p.kvflags & FORGE_NORM_QK, p.kw, p.eps, cr, sr, li);
+        const uint4 nv = new_row_slice<T, D>(load16(vr), p.kvflags & FORGE_NORM_V, nullptr, p.eps,
+                                             nullptr, nullptr, li);
+        if (pp <= n_hi) {
+          store16(static_cast<T*>(p.kcw) + slab + (int64_t)pp * p.sks + li * VEC, nk);
+          store16(static_cast<T*>(p.vcw) + slab + (int64_t)pp * p.sks + li * VEC, nv);
+        }
       }
+      // the stores complete before the stream below loads the same rows
+      __builtin_amdgcn_s_waitcnt(0);
+      asm volatile("" ::: "memory");
+    }
   }
 
   int it_first = kmin_rb > c0 ? (kmin_rb - c0) / KPI : 0;
@@ -509,26 +505,9 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
     for (int e = 0; e < VEC; ++e) o[r][e] = 0.0f;
   }
 
-  auto compute_iter = [&](int it, const uint4* kin, const uint4* vin) {
+  auto compute_iter = [&](int it, const uint4* kr, const uint4* vr) {
     const int kb0 = c0 + it * KPI;
     const bool full = kb0 >= lo_all && kb0 + KPI - 1 <= hi_all;  // every row sees every key
-    uint4 kr[NK], vr[NK];
-#pragma unroll
-    for (int u = 0; u < NK; ++u) {
-      kr[u] = kin[u];
-      vr[u] = vin[u];
-    }
-    if (has_new && kb0 <= n_hi && kb0 + KPI - 1 >= n_lo) {  // block-uniform
-      // the new keys and values stand in for the cache rows, which hold older data
-#pragma unroll
-      for (int u = 0; u < NK; ++u)
-#pragma unroll
-        for (int j = 0; j < kNewPerLane; ++j)
-          if (kb0 + u * NG + g == new_pos[j]) {
-            kr[u] = new_k[j];
-            vr[u] = new_v[j];
-          }
-    }
     float s[ROWS][NK];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
@@ -689,7 +668,10 @@ void splitk_kernel(SplitParams p) {
   if (!p.persist) {
     // Positions fit in 32 bits (host check: max_len < 2^30).
     const int base = (int)row_base(p.row_pos, p.pos_dev, p.pos0, blockIdx.z);
-    split_unit<T, D, ROWS>(p, blockIdx.z, base, blockIdx.y % p.K, blockIdx.y / p.K, blockIdx.x, sh);
+    // chunks in reverse: a row's last chunk, whose unit also makes the step's new keys
+    // (forge_attn_decode_append) and so starts its stream later, is dispatched first
+    split_unit<T, D, ROWS>(p, blockIdx.z, base, blockIdx.y % p.K, blockIdx.y / p.K,
+                           (int)gridDim.x - 1 - (int)blockIdx.x, sh);
     return;
   }
   __shared__ int sh_pref[kPersistMaxRows + 1];
@@ -760,7 +742,8 @@ void splitk_kernel(SplitParams p) {
     const int base = __builtin_amdgcn_readfirstlane(sh_base[lo]);
     int kmin, kmax;
     visible_range32(base, p.window, (int)p.max_len, kmin, kmax);  // the row's first chunk
-    split_unit<T, D, ROWS>(p, lo, base, pr % p.K, pr / p.K, kmin / p.chunk + o % n, sh, &next);
+    // a row's chunks last to first (the last one's unit also makes the new keys)
+    split_unit<T, D, ROWS>(p, lo, base, pr % p.K, pr / p.K, kmin / p.chunk + (n - 1 - o % n), sh, &next);
     if (tid == 0) sh_ticket[parity] = (int)gridDim.x + next;
     __syncthreads();  // the next unit reuses the merge LDS; the ticket is visible
   }
@@ -1361,12 +1344,19 @@ static int auto_chunk(int dtype, int B, int /*T*/, int H, int K, int D, int64_t 
   const int64_t n_rb = (G * T + rows - 1) / rows;
   const int64_t pairs = (int64_t)B * K * n_rb;
   // At least 4 block iterations per unit (a one-iteration unit spends most of its time in
-  // the q prologue and the merge), then larger while about 2048 units remain.
+  // the q prologue and the merge), then larger while at least one unit per CU remains:
+  // fewer, longer units spend less on prologues, merges and partials (C2, 64 (row, KV
+  // head) pairs of 2049 keys: 512-key chunks, 320 units, 23.4 us per call against 24.7 us
+  // at 256 and 24.4 us at 1024).
   const int kpi = keys_per_iter(dtype, D);
   int chunk = kpi;
   const int64_t len = max_kv_len > 0 ? max_kv_len : 1;
+  int ncu = 0, dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+    ncu = 256;
   while (chunk * 2 <= kMaxChunk &&
-         (chunk < 4 * kpi || pairs * ((len + chunk * 2 - 1) / (chunk * 2)) >= 2048))
+         (chunk < 4 * kpi || pairs * ((len + chunk * 2 - 1) / (chunk * 2)) >= ncu))
     chunk *= 2;
   return chunk;
 }
@@ -1676,10 +1666,12 @@ extern "C" int forge_attn_decode_append(
   const int vec = vec_of(dtype);
   const size_t need = decode_need(p, D);
   if (need && (!workspace || workspace_bytes < need)) return set_error("workspace too small");
-  // In the split-K kernel when a lane group holds at most kNewPerLane new keys and the rows
+  // In the split-K kernel when one row block holds a KV head's G*T query rows (one unit per
+  // chunk reads the new rows), a lane group holds at most kNewPerLane new keys and the rows
   // allow 16-byte slices; otherwise (the MFMA path among them) forge_kv_append runs first.
   const int groups = kSplitThreads / (D / vec);
   const bool fused = !use_verify_mfma(dtype, D, p.G) && T <= kNewPerLane * groups &&
+                     rows_per_block(p.rows_total) >= p.rows_total &&
                      ((uintptr_t)k | (uintptr_t)v | (uintptr_t)k_weight | (uintptr_t)cos | (uintptr_t)sin) % 16 == 0 &&
                      (sknb | sknh | sknt | svnb | svnh | svnt) % vec == 0;
   if (!fused) {
