@@ -118,10 +118,10 @@ int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, const void* 
  * at base_b + t (KVCache.update, kv_cache.py:52-60; StaticKVCache.update 107-114), and
  * attended to: the split-K unit whose chunk holds a new position makes that key and value,
  * writes them and then streams its chunk. The keys, values and outputs are those of the two
- * calls, bit for bit. Where a KV head's G*T query rows need more than one row block, a lane
- * group would hold more than two new keys, or on the wide-group MFMA path (G >= 4,
- * bf16/fp16, D 128/256), it issues forge_kv_append's kernel first. Other arguments and the
- * workspace as forge_attn_decode.
+ * calls, bit for bit. Where a KV head's G*T query rows need more than one row block (8 rows
+ * on the split-K path, 32 on the wide-group MFMA path: G >= 4, bf16/fp16, D 128/256) or a
+ * lane group would hold more than two new keys, it issues forge_kv_append's kernel first.
+ * Other arguments and the workspace as forge_attn_decode.
  */
 int forge_attn_decode_append(int dtype, int B, int T, int H, int K, int D, const void* q,
                              int64_t sqb, int64_t sqh, int64_t sqt, const float* q_weight,

@@ -939,6 +939,41 @@ void verify_mfma_kernel(SplitParams p) {
   const int c = p.span_chunks ? umin / p.chunk + (int)blockIdx.x : (int)blockIdx.x;  // absolute chunk
   const int c0 = c * p.chunk;
   if (c >= p.max_chunks || c0 > umax || c0 + p.chunk - 1 < umin) return;  // block-uniform
+
+  // New positions in this chunk (forge_attn_decode_append; the host takes this path when the
+  // unit's row block holds all of the KV head's query rows, so this block is the only reader
+  // of these cache rows): make them (a group of D / 8 lanes per row), write them, and wait
+  // for every wave's writes before any tile load.
+  if (p.kn) {
+    int n_lo = base > c0 ? base : c0;
+    int n_hi = base + p.T - 1 < c0 + p.chunk - 1 ? base + p.T - 1 : c0 + p.chunk - 1;
+    if (n_hi > (int)p.max_len - 1) n_hi = (int)p.max_len - 1;
+    if (n_lo <= n_hi) {  // block-uniform
+      constexpr int VEC = 16 / sizeof(T);
+      constexpr int LPR = D / VEC;
+      constexpr int RPP = 256 / LPR;  // rows per pass of the block
+      const int li = tid % LPR, rr = tid / LPR;
+      const int64_t slab = b * p.skb + kvh * p.skh;
+      for (int p0 = n_lo; p0 <= n_hi; p0 += RPP) {
+        const int pp = p0 + rr;
+        const int tt = (pp <= n_hi ? pp : n_hi) - base;  // a row of the call, for every lane
+        const T* kr = static_cast<const T*>(p.kn) + b * p.sknb + kvh * p.sknh + tt * p.sknt + li * VEC;
+        const T* vr = static_cast<const T*>(p.vn) + b * p.svnb + kvh * p.svnh + tt * p.svnt + li * VEC;
+        const bool krope = p.kvflags & FORGE_ROPE;
+        const float* cr = krope ? p.cos + b * p.csb + tt * p.cst : nullptr;
+        const float* sr = krope ? p.sin + b * p.csb + tt * p.cst : nullptr;
+        const uint4 nk = new_row_slice<T, D>(load16(kr), p.kvflags & FORGE_NORM_QK, p.kw, p.eps, cr, sr, li);
+        const uint4 nv = new_row_slice<T, D>(load16(vr), p.kvflags & FORGE_NORM_V, nullptr, p.eps,
+                                             nullptr, nullptr, li);
+        if (pp <= n_hi) {
+          store16(static_cast<T*>(p.kcw) + slab + (int64_t)pp * p.sks + li * VEC, nk);
+          store16(static_cast<T*>(p.vcw) + slab + (int64_t)pp * p.sks + li * VEC, nv);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  }
   int t_first = umin > c0 ? (umin - c0) / BN : 0;
   int t_last = (umax - c0) / BN;
   if (t_last > p.chunk / BN - 1) t_last = p.chunk / BN - 1;
@@ -1666,12 +1701,15 @@ extern "C" int forge_attn_decode_append(
   const int vec = vec_of(dtype);
   const size_t need = decode_need(p, D);
   if (need && (!workspace || workspace_bytes < need)) return set_error("workspace too small");
-  // In the split-K kernel when one row block holds a KV head's G*T query rows (one unit per
-  // chunk reads the new rows), a lane group holds at most kNewPerLane new keys and the rows
-  // allow 16-byte slices; otherwise (the MFMA path among them) forge_kv_append runs first.
+  // In the attention kernel when one row block holds a KV head's G*T query rows (one unit
+  // per chunk reads the new rows; on the split-K path a lane group also holds at most
+  // kNewPerLane new keys) and the rows allow 16-byte slices; otherwise forge_kv_append's
+  // kernel runs first.
   const int groups = kSplitThreads / (D / vec);
-  const bool fused = !use_verify_mfma(dtype, D, p.G) && T <= kNewPerLane * groups &&
-                     rows_per_block(p.rows_total) >= p.rows_total &&
+  const bool one_block = use_verify_mfma(dtype, D, p.G)
+                             ? p.rows_total <= kVerifyRows
+                             : T <= kNewPerLane * groups && rows_per_block(p.rows_total) >= p.rows_total;
+  const bool fused = one_block &&
                      ((uintptr_t)k | (uintptr_t)v | (uintptr_t)k_weight | (uintptr_t)cos | (uintptr_t)sin) % 16 == 0 &&
                      (sknb | sknh | sknt | svnb | svnh | svnt) % vec == 0;
   if (!fused) {

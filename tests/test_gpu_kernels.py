@@ -380,10 +380,12 @@ def test_decode_append_equals_append_then_decode(dtype, D, HK):
 def test_decode_append_verify_steps(T, window, where):
     """Verify steps of T new tokens (the new keys may straddle a chunk boundary: 64-key
     chunks, the new keys at 510 .. 510 + T - 1), host, per-row and device positions, and
-    a values norm: equal to the two calls bit for bit."""
+    a values norm: equal to the two calls bit for bit. The last case is the MFMA verify
+    path (MQA, hd 256: 32 query rows of one KV head in one unit up to T = 4, two launches
+    beyond)."""
     lens = [510 + T] * 3 if where != "row_pos" else [T, 510 + T, 900]
     for dtype, D, (H, K) in ((torch.bfloat16, 128, (16, 8)), (torch.float32, 64, (12, 4)),
-                             (torch.float16, 256, (4, 2))):
+                             (torch.float16, 256, (4, 2)), (torch.bfloat16, 256, (8, 1))):
         a, b, _ = _append_decode_pair(T + window, dtype, 3, H, K, D, T, lens, window, where,
                                       norm_v=(T == 5), chunk=64 if D < 256 else 128)
         for x, y in zip(a, b):
