@@ -76,7 +76,9 @@ class DecodeWorkload:
 
         self.chunk = ops.decode_chunk(dtype, B, T, H, K, D, self.max_len, window)
         nbytes = ops.decode_workspace_bytes(dtype, B, T, H, K, D, self.max_len, self.chunk)
-        self.ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        # cleared once: each call leaves the persistent grid's work ticket zero, as the
+        # module's per-stream workspace does (no ticket-reset kernel per step)
+        self.ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=dev)
         self.layer = 0
 
     def append(self, layer=None):
@@ -110,7 +112,7 @@ class DecodeWorkload:
         ops.attn_decode_append(self.q, self.k, self.v, self.k_caches[i], self.v_caches[i], scale=self.scale,
                                **where, max_kv_len=self.max_len, window=self.window, q_weight=self.wq,
                                k_weight=self.wk, eps=1e-6, norm_q=True, norm_k=True, cos=cos, sin=sin,
-                               chunk=self.chunk, out=self.out, workspace=self.ws)
+                               chunk=self.chunk, out=self.out, workspace=self.ws, workspace_zeroed=True)
         self.layer = (self.layer + 1) % len(self.k_caches)
 
     def step_two_pass(self):

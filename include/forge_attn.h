@@ -121,8 +121,13 @@ int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, const void* 
  * calls, bit for bit. Where a KV head's G*T query rows need more than one row block (8 rows
  * on the split-K path, 32 on the wide-group MFMA path: G >= 4, bf16/fp16, D 128/256) or a
  * lane group would hold more than two new keys, it issues forge_kv_append's kernel first.
- * Other arguments and the workspace as forge_attn_decode.
+ * Other arguments and the workspace as forge_attn_decode. ws_flags = FORGE_WS_ZEROED
+ * promises that the workspace's first 4 bytes (the persistent grid's work ticket) hold zero,
+ * which saves the small kernel that otherwise zeroes them; every call leaves them zero, so a
+ * workspace cleared once before its first use keeps the promise for the calls that follow it
+ * on one stream.
  */
+#define FORGE_WS_ZEROED 1 /* ws_flags: the workspace's first 4 bytes hold zero */
 int forge_attn_decode_append(int dtype, int B, int T, int H, int K, int D, const void* q,
                              int64_t sqb, int64_t sqh, int64_t sqt, const float* q_weight,
                              float eps, int flags, const void* k, int64_t sknb, int64_t sknh,
@@ -134,7 +139,7 @@ int forge_attn_decode_append(int dtype, int B, int T, int H, int K, int D, const
                              const int64_t* pos_dev, int64_t pos0, int64_t max_kv_len,
                              int window, float scale, int chunk, void* out, int64_t sob,
                              int64_t sot, int64_t soh, void* workspace, size_t workspace_bytes,
-                             void* stream);
+                             int ws_flags, void* stream);
 /*
  * Allocation-free forge_attn_decode (no counterpart in the reference). For callers that
  * cannot allocate device memory: code under graph capture that may not call hipMalloc,

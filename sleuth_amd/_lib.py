@@ -17,6 +17,7 @@ ABI_VERSION = 2
 F32, BF16, F16 = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 48 * 1024 * 1024   # FORGE_NOALLOC_SCRATCH_BYTES
 NORM_QK, ROPE, NORM_V = 1, 2, 4
+WS_ZEROED = 1                              # FORGE_WS_ZEROED
 
 _p = C.c_void_p
 _i = C.c_int
@@ -65,7 +66,7 @@ SIGNATURES: dict[str, tuple] = {
         _p, _p, _i64, _i64,                  # row_pos, pos_dev, pos0, max_kv_len
         _i, _f, _i,                          # window, scale, chunk
         _p, _i64, _i64, _i64,                # out + strides (b, t, h)
-        _p, C.c_size_t,                      # workspace, bytes
+        _p, C.c_size_t, _i,                  # workspace, bytes, ws_flags
         _p]),
     "forge_attn_decode_noalloc": (_i, [
         _i, _i, _i, _i, _i, _i,              # dtype, B, T, H, K, D

@@ -82,7 +82,8 @@ struct SplitParams {
                     // 0: blockIdx.x is the absolute chunk
   float2* ws_ml;  // [B*H*T][max_chunks] (m, l)
   float* ws_o;    // [B*H*T][max_chunks][D]
-  int* ws_ctr;    // work ticket of the persistent grid (zeroed before each launch), or null
+  int* ws_ctr;    // work ticket of the persistent grid (zero when the split kernel starts), or null
+  int ws_zeroed;  // 1: the caller's workspace already holds a zero ticket (no reset kernel)
   // The new tokens' raw keys and values (forge_attn_decode_append), or null: the unit whose
   // chunk holds a new position makes that key (norm + RoPE) and value (norm), writes them
   // into the cache and then streams its chunk (one row block per KV head: the only reader).
@@ -766,6 +767,9 @@ __global__ __launch_bounds__(256) void combine_kernel(SplitParams p) {
   __shared__ float sh_m[NWAVES], sh_l[NWAVES];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
+  // the split kernel has finished with the work ticket: leave it zero for the next call on
+  // this workspace (FORGE_WS_ZEROED)
+  if (blockIdx.x == 0 && threadIdx.x == 0 && p.ws_ctr) *p.ws_ctr = 0;
   const int64_t row = blockIdx.x;  // == (b*H + h)*T + t
   const int t = (int)(row % p.T);
   const int b = (int)(row / ((int64_t)p.T * p.H));
@@ -1460,9 +1464,11 @@ static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
       return set_error("forge_attn_decode: too many work units");
     p.persist = 1;
     grid = dim3((unsigned)blocks);
-    hipLaunchKernelGGL(ticket_reset_kernel, dim3(1), dim3(64), 0, s, p.ws_ctr);
-    const int st0 = check_launch();
-    if (st0) return st0;
+    if (!p.ws_zeroed) {
+      hipLaunchKernelGGL(ticket_reset_kernel, dim3(1), dim3(64), 0, s, p.ws_ctr);
+      const int st0 = check_launch();
+      if (st0) return st0;
+    }
   } else {
     if ((int64_t)p.K * n_rb > 65535 || p.B > 65535) return set_error("grid too large");
     p.persist = 0;
@@ -1531,8 +1537,8 @@ extern "C" int forge_attn_decode_chunk(int dtype, int B, int T, int H, int K, in
   return auto_chunk(dtype, B, T, H, K, D, max_kv_len);
 }
 
-// Workspace of a call with `slots` (row, chunk) partials: fp32 (m, l) pairs, fp32 partial
-// outputs, and the persistent grid's work ticket.
+// Workspace of a call with `slots` (row, chunk) partials: the persistent grid's work ticket
+// (256 bytes), fp32 (m, l) pairs and fp32 partial outputs.
 static size_t workspace_for(int64_t slots, int D) {
   const size_t ml = ((size_t)slots * sizeof(float2) + 255) / 256 * 256;
   const size_t o = ((size_t)slots * D * sizeof(float) + 255) / 256 * 256;
@@ -1634,15 +1640,16 @@ size_t decode_need(const SplitParams& p, int D) {
   return p.max_chunks > 1 ? workspace_for((int64_t)p.B * p.H * p.T * p.max_chunks, D) : 0;
 }
 
-// Points p's partials and work ticket into `ws` (at least decode_need bytes).
+// Points p's work ticket and partials into `ws` (at least decode_need bytes). The ticket sits
+// at offset 0 for every shape, so a workspace reused by calls of different shapes keeps it
+// in one place (the combine kernel leaves it zero: FORGE_WS_ZEROED).
 void decode_bind(SplitParams& p, int D, void* ws) {
   if (p.max_chunks < 2) return;
   const int64_t slots = (int64_t)p.B * p.H * p.T * p.max_chunks;
   const size_t ml = ((size_t)slots * sizeof(float2) + 255) / 256 * 256;
-  const size_t o = ((size_t)slots * D * sizeof(float) + 255) / 256 * 256;
-  p.ws_ml = static_cast<float2*>(ws);
-  p.ws_o = reinterpret_cast<float*>(static_cast<char*>(ws) + ml);
-  p.ws_ctr = reinterpret_cast<int*>(static_cast<char*>(ws) + ml + o);
+  p.ws_ctr = static_cast<int*>(ws);
+  p.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + 256);
+  p.ws_o = reinterpret_cast<float*>(static_cast<char*>(ws) + 256 + ml);
 }
 
 int decode_launch(const SplitParams& p, int dtype, int D, hipStream_t s) {
@@ -1689,7 +1696,7 @@ extern "C" int forge_attn_decode_append(
     int64_t s_cos_t, void* k_cache, void* v_cache, int64_t skb, int64_t skh, int64_t sks,
     int64_t max_len, const int32_t* row_pos, const int64_t* pos_dev, int64_t pos0,
     int64_t max_kv_len, int window, float scale, int chunk, void* out, int64_t sob, int64_t sot,
-    int64_t soh, void* workspace, size_t workspace_bytes, void* stream) {
+    int64_t soh, void* workspace, size_t workspace_bytes, int ws_flags, void* stream) {
   clear_error();
   SplitParams p;
   int st = decode_setup(p, dtype, B, T, H, K, D, q, sqb, sqh, sqt, q_weight, eps, flags, cos, sin,
@@ -1732,6 +1739,7 @@ extern "C" int forge_attn_decode_append(
     p.vcw = v_cache;
   }
   decode_bind(p, D, workspace);
+  p.ws_zeroed = (ws_flags & FORGE_WS_ZEROED) ? 1 : 0;
   return decode_launch(p, dtype, D, (hipStream_t)stream);
 }
 

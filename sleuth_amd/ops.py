@@ -14,7 +14,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from ._lib import BF16, F16, F32, NORM_QK, NORM_V, ROPE, check, lib
+from ._lib import BF16, F16, F32, NORM_QK, NORM_V, ROPE, WS_ZEROED, check, lib
 
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -231,6 +231,21 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *
     return out
 
 
+_STREAM_WS: dict = {}
+
+
+def _stream_workspace(dev: torch.device, need: int) -> torch.Tensor:
+    """A split-K workspace per (device, stream), cleared when it is made: every call leaves
+    its work ticket zero, so calls ordered on that stream may skip the ticket reset. Grown
+    (a new cleared buffer) when a call needs more."""
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    ws = _STREAM_WS.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=dev)
+        _STREAM_WS[key] = ws
+    return ws
+
+
 def attn_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
                        v_cache: torch.Tensor, *, scale: float, pos: int | None = None,
                        pos_dev: torch.Tensor | None = None, row_pos: torch.Tensor | None = None,
@@ -239,10 +254,13 @@ def attn_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cach
                        eps: float = 1e-6, norm_q: bool = False, norm_k: bool = False,
                        norm_v: bool = False, cos: torch.Tensor | None = None,
                        sin: torch.Tensor | None = None, chunk: int = 0, out: torch.Tensor | None = None,
-                       workspace: torch.Tensor | None = None) -> torch.Tensor:
+                       workspace: torch.Tensor | None = None, workspace_zeroed: bool = False) -> torch.Tensor:
     """kv_append(k, v, ...) then attn_decode(q, ...), as one forge_attn_decode_append call:
     the new keys (norm_k with k_weight, RoPE) and values (norm_v) go into the cache at
-    base_b + t and the T queries attend over it, the new keys included. Returns [B,T,H,D]."""
+    base_b + t and the T queries attend over it, the new keys included. Returns [B,T,H,D].
+    Without a workspace (and outside graph capture) the call uses this module's zeroed
+    workspace for the current stream (FORGE_WS_ZEROED: no ticket-reset kernel);
+    workspace_zeroed=True makes the same promise for a workspace the caller cleared once."""
     B, K, T, D = k.shape
     if v.shape != k.shape or q.shape[0] != B or q.shape[2] != T or q.shape[3] != D:
         raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)} and v {tuple(v.shape)} do not fit")
@@ -262,12 +280,16 @@ def attn_decode_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cach
     kv_flags = (NORM_QK if norm_k else 0) | (ROPE if c is not None else 0) | (NORM_V if norm_v else 0)
     kw = _weight(k_weight, D) if norm_k else None
     need = lib().forge_attn_decode_workspace_bytes(args[0], B, T, q.shape[1], K, D, max_kv_len, chunk)
+    zeroed = bool(workspace_zeroed)
+    if need and workspace is None and not torch.cuda.is_current_stream_capturing():
+        workspace, zeroed = _stream_workspace(dev, need), True
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        workspace, zeroed = torch.empty(need, dtype=torch.uint8, device=dev), False
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     st = lib().forge_attn_decode_append(*args[:13], _ptr(k), k.stride(0), k.stride(1), k.stride(2),
                                         _ptr(v), v.stride(0), v.stride(1), v.stride(2), _ptr(kw), kv_flags,
-                                        *args[13:], _ptr(workspace), ws_bytes, _stream(dev))
+                                        *args[13:], _ptr(workspace), ws_bytes, WS_ZEROED if zeroed else 0,
+                                        _stream(dev))
     check(st, "forge_attn_decode_append")
     return out
 

@@ -408,3 +408,26 @@ def test_decode_append_against_the_oracle():
         assert (kc[b, :, L:].cpu() == 1e4).all() and (vc[b, :, L:].cpu() == 1e4).all()
     ref = oracle.ragged_decode(qn.float(), kc.float().cpu(), vc.float().cpu(), lens, 0, scale_of(D))
     assert max_abs(y, ref.transpose(1, 2)) <= 2e-2
+
+
+def test_decode_append_with_a_cleared_workspace_across_calls():
+    """FORGE_WS_ZEROED: a workspace cleared once, reused by calls of different shapes on the
+    persistent grid (per-row lengths) without the ticket-reset kernel, gives the results of
+    calls that reset it, bit for bit, and is left with a zero ticket after each call."""
+    o = ops()
+    ws = torch.zeros(8 << 20, dtype=torch.uint8, device=DEV)
+    for i, (B, H, K, D, T, lens) in enumerate([(6, 16, 8, 128, 1, [900, 40, 3000, 1, 2200, 700]),
+                                               (3, 12, 4, 64, 4, [515, 2049, 64]),
+                                               (6, 16, 8, 128, 1, [901, 41, 3001, 2, 2201, 701])]):
+        a, b, (q, k, v, wq, wk, c, s) = _append_decode_pair(40 + i, torch.bfloat16, B, H, K, D, T, lens, 0,
+                                                            "row_pos", chunk=64)
+        kc, vc = a[1].clone(), a[2].clone()
+        base = [L - T for L in lens]
+        # rewind the rows the pair already wrote (the fused call writes them again)
+        y = o.attn_decode_append(q, k, v, kc, vc, scale=scale_of(D),
+                                 row_pos=torch.tensor(base, dtype=torch.int32, device=DEV),
+                                 max_kv_len=kc.shape[2], q_weight=wq, k_weight=wk, eps=1e-6, norm_q=True,
+                                 norm_k=True, cos=c, sin=s, chunk=64, workspace=ws, workspace_zeroed=True)
+        torch.cuda.synchronize()
+        assert torch.equal(y, a[0]) and torch.equal(kc, a[1]) and torch.equal(vc, a[2]), i
+        assert int(ws[:4].view(torch.int32).item()) == 0, i
