@@ -232,17 +232,21 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *
 
 
 _STREAM_WS: dict = {}
+_STREAM_WS_MAX = 16   # streams whose workspace is kept (the oldest is dropped beyond that)
 
 
 def _stream_workspace(dev: torch.device, need: int) -> torch.Tensor:
     """A split-K workspace per (device, stream), cleared when it is made: every call leaves
     its work ticket zero, so calls ordered on that stream may skip the ticket reset. Grown
-    (a new cleared buffer) when a call needs more."""
+    (a new cleared buffer) when a call needs more. Dropping a buffer is safe while its calls
+    are in flight: torch's allocator reuses the memory only in that stream's order."""
     key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
-    ws = _STREAM_WS.get(key)
+    ws = _STREAM_WS.pop(key, None)
     if ws is None or ws.numel() < need:
         ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=dev)
-        _STREAM_WS[key] = ws
+    _STREAM_WS[key] = ws   # most recently used last
+    while len(_STREAM_WS) > _STREAM_WS_MAX:
+        _STREAM_WS.pop(next(iter(_STREAM_WS)))
     return ws
 
 
