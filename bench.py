@@ -74,7 +74,7 @@ class DecodeWorkload:
         self.out = torch.empty(B, T, H, D, device=dev, dtype=dtype)
         from sleuth_amd import ops
 
-        self.chunk = ops.decode_chunk(dtype, B, T, H, K, D, self.max_len, window)
+        self.chunk = ops.decode_chunk(dtype, B, T, H, K, D, self.max_len, window, uniform=self.pos is not None)
         nbytes = ops.decode_workspace_bytes(dtype, B, T, H, K, D, self.max_len, self.chunk)
         # cleared once: each call leaves the persistent grid's work ticket zero, as the
         # module's per-stream workspace does (no ticket-reset kernel per step)

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define FORGE_ABI_VERSION 2
+#define FORGE_ABI_VERSION 3
 
 /* dtype codes */
 #define FORGE_F32 0
@@ -166,6 +166,14 @@ int forge_attn_decode_noalloc(int dtype, int B, int T, int H, int K, int D, cons
 /* Keys per split for a row span of max_kv_len keys (pure host function). T is accepted
  * for the signature but does not enter, so decode and verify steps of one layer agree. */
 int forge_attn_decode_chunk(int dtype, int B, int T, int H, int K, int D, int64_t max_kv_len);
+
+/* Keys per split for calls whose rows all start at one host position (pos0, no row_pos or
+ * pos_dev): every row has the same length, so the split only has to spread the work over
+ * the CUs, and rows are not split at all when the (row, KV head) pairs already fill them.
+ * Use it for such calls in place of forge_attn_decode_chunk (no counterpart in the
+ * reference: a tuning query, like forge_attn_decode_chunk). T does not enter. */
+int forge_attn_decode_chunk_uniform(int dtype, int B, int T, int H, int K, int D,
+                                    int64_t max_kv_len);
 
 /* Workspace bytes forge_attn_decode needs (pure host function). */
 size_t forge_attn_decode_workspace_bytes(int dtype, int B, int T, int H, int K, int D,

@@ -12,7 +12,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libforge_attn.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, BF16, F16 = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 48 * 1024 * 1024   # FORGE_NOALLOC_SCRATCH_BYTES
@@ -79,6 +79,7 @@ SIGNATURES: dict[str, tuple] = {
         _p, _i64, _i64, _i64,                # out + strides (b, t, h)
         _p]),                                # stream
     "forge_attn_decode_chunk": (_i, [_i, _i, _i, _i, _i, _i, _i64]),
+    "forge_attn_decode_chunk_uniform": (_i, [_i, _i, _i, _i, _i, _i, _i64]),
     "forge_attn_decode_workspace_bytes": (C.c_size_t, [_i, _i, _i, _i, _i, _i, _i64, _i]),
     "forge_attn_prefill": (_i, [
         _i, _i, _i, _i, _i, _i,              # dtype, B, T, H, K, D

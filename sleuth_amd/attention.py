@@ -241,7 +241,6 @@ class Attention(nn.Module):
             pos_kw, max_kv, offset, chunk = dict(pos=0), T, 0, 0
         else:
             kc, vc = cache.k[self.layer_idx], cache.v[self.layer_idx]
-            chunk = ops.decode_chunk(q.dtype, B, 1, H, self.n_kv, hd, cache.max_len, self.window)
             if getattr(cache, "static", False):
                 # StaticKVCache (kv_cache.py:73-138): positions pos_t + arange(T) on the device
                 pos_kw, max_kv, offset = dict(pos_dev=cache.positions), min(cache.length, cache.max_len), None
@@ -256,6 +255,10 @@ class Attention(nn.Module):
                     pos_kw, max_kv, offset = dict(row_pos=rows), top + T, None
                 else:
                     pos_kw, max_kv, offset = dict(pos=cache.pos), cache.pos + T, cache.pos
+            # from the cache's capacity and T = 1: every step of this layer, decode or verify,
+            # splits its rows at the same keys
+            chunk = ops.decode_chunk(q.dtype, B, 1, H, self.n_kv, hd, cache.max_len, self.window,
+                                     uniform="pos" in pos_kw)
 
         if T > DECODE_MAX_T and offset is not None and ops.prefill_supported(q) and \
                 (q_args["cos"] is None or q_args["cos"].dim() == 2):

@@ -78,7 +78,7 @@ class GatedAttention(nn.Module):
                 raise ValueError(f"KV cache full: pos {cache.pos} + {T} > max_len {cache.max_len}")
             kc, vc = cache.k[self.layer_idx], cache.v[self.layer_idx]
             offset = cache.pos
-            chunk = ops.decode_chunk(q.dtype, B, 1, H, K, hd, cache.max_len, 0)
+            chunk = ops.decode_chunk(q.dtype, B, 1, H, K, hd, cache.max_len, 0, uniform=True)
         ops.kv_append(k, v, kc, vc, pos=offset)
         scale = hd ** -0.5
         if T > DECODE_MAX_T and ops.prefill_supported(q):

@@ -23,14 +23,15 @@ def declared() -> set[str]:
 
 def test_library_loads_with_abi_version():
     lib = _lib.lib()
-    assert lib.forge_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.forge_abi_version() == _lib.ABI_VERSION == 3
     assert lib.forge_last_error() == b""
 
 
 def test_every_declared_symbol_is_exported_and_bound():
     names = declared()
     assert {"forge_abi_version", "forge_last_error", "forge_head_norm_rope", "forge_kv_append",
-            "forge_attn_decode", "forge_attn_decode_append", "forge_attn_decode_chunk", "forge_attn_decode_workspace_bytes",
+            "forge_attn_decode", "forge_attn_decode_append", "forge_attn_decode_chunk",
+            "forge_attn_decode_chunk_uniform", "forge_attn_decode_workspace_bytes",
             "forge_attn_prefill"} <= names
     raw = C.CDLL(str(_lib.LIB_PATH))
     for n in names:
@@ -48,6 +49,28 @@ def test_host_only_functions():
     assert ws >= 64 * 16 * chunks * (128 * 4 + 8)
     assert lib.forge_attn_decode_workspace_bytes(_lib.BF16, 1, 1, 8, 4, 64, 50, 64) == 0  # one chunk
     assert lib.forge_attn_decode_chunk(_lib.BF16, 1, 1, 8, 3, 64, 100) == 0              # H % K != 0
+
+
+def test_uniform_chunk_rule():
+    """One host position for every row: chunks sized so the CUs get equal work, no split when
+    the (row, KV head) pairs fill them (this container has no GPU: 256 CUs assumed, as on
+    MI355X)."""
+    lib = _lib.lib()
+    ch = lambda B, H, K, D, L, dt=_lib.BF16: lib.forge_attn_decode_chunk_uniform(dt, B, 1, H, K, D, L)
+    assert ch(32, 16, 8, 128, 8192) == 8192      # C3 decode: 256 pairs, one unit per CU
+    assert ch(64, 16, 8, 128, 4096) == 4096      # 512 pairs: two per CU, still no split
+    assert ch(48, 16, 8, 128, 8192) == 4096      # 384 pairs: 768 units = 3 per CU
+    assert ch(24, 16, 8, 128, 8192) == 2048      # 192 pairs: 768 units
+    assert ch(16, 12, 4, 64, 2049) == 576        # C2: 64 pairs x 4 chunks = 256 units
+    assert ch(1, 8, 4, 64, 50) == 64             # one short row: one chunk of one iteration
+    for B, H, K, D, L in [(32, 16, 8, 128, 8192), (16, 12, 4, 64, 2049), (3, 8, 2, 32, 777),
+                          (100, 8, 8, 256, 70000)]:
+        c = ch(B, H, K, D, L)
+        kpi = (256 // (D // 8)) * 2
+        assert c % kpi == 0 and c >= min(4 * kpi, -(-L // kpi) * kpi)
+    # the MFMA verify shapes (G >= 4, hd 128/256, bf16/fp16) keep their own rule
+    assert ch(8, 8, 1, 256, 8196) == lib.forge_attn_decode_chunk(_lib.BF16, 8, 1, 8, 1, 256, 8196)
+    assert ch(1, 8, 3, 64, 100) == 0             # H % K != 0
 
 
 def _decode_args(**over):
