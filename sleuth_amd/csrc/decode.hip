@@ -40,7 +40,7 @@ namespace forge {
 #endif
 constexpr int kSplitThreads = 256;
 constexpr int kSplitNK = FORGE_SPLIT_NK;  // keys per group per iteration
-constexpr int kMaxChunk = 512;
+constexpr int kMaxChunk = 1024;
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale: weights stay <= 2^8
 // Register buffers of the K/V pipeline (loads run PF - 1 iterations ahead): deeper where
 // few query rows leave the registers for it. Measured on C4-shaped ragged decode: PF 4
@@ -1388,10 +1388,10 @@ static int auto_chunk(int dtype, int B, int /*T*/, int H, int K, int D, int64_t 
   const int64_t n_rb = (G * T + rows - 1) / rows;
   const int64_t pairs = (int64_t)B * K * n_rb;
   // At least 4 block iterations per unit (a one-iteration unit spends most of its time in
-  // the q prologue and the merge), then larger while at least one unit per CU remains:
-  // fewer, longer units spend less on prologues, merges and partials (C2, 64 (row, KV
-  // head) pairs of 2049 keys: 512-key chunks, 320 units, 23.4 us per call against 24.7 us
-  // at 256 and 24.4 us at 1024).
+  // the q prologue and the merge), then larger, up to 1024 keys, while at least one unit
+  // per CU remains: fewer, longer units spend less on prologues, merges and partials, and
+  // the cap keeps the units a ragged batch's longest rows leave for the end short (C4 step:
+  // 609.5 us at 1024-key chunks, 610.6 at 768, 615.0 at 512; attention call 630 us at 2048).
   const int kpi = keys_per_iter(dtype, D);
   int chunk = kpi;
   const int64_t len = max_kv_len > 0 ? max_kv_len : 1;

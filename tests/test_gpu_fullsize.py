@@ -76,7 +76,7 @@ def test_c3_prefill_full_size():
     _argmax_ok(got, ref)
 
 
-def _decode_full(lens, H, K, D, theta, seed, sample=None):
+def _decode_full(lens, H, K, D, theta, seed, sample=None, chunk=0):
     """Ragged decode through forge_kv_append + forge_attn_decode at the benchmark's layout:
     caches [B, K, max(lens), D], rows prefilled with N(0,1) up to L_b - 1, the new token
     appended at L_b - 1 (norm + RoPE fused), everything past L_b holding 1e4.
@@ -105,7 +105,7 @@ def _decode_full(lens, H, K, D, theta, seed, sample=None):
     ops().kv_append(kn.to(DEV), vn.to(DEV), kc, vc, **where, k_weight=wk.to(DEV), eps=1e-6, norm_k=True,
                     cos=c, sin=s_)
     got = ops().attn_decode(q.to(DEV), kc, vc, scale=sc, **where, max_kv_len=max_len, q_weight=wq.to(DEV),
-                            eps=1e-6, norm_q=True, cos=c, sin=s_).float().cpu()
+                            eps=1e-6, norm_q=True, cos=c, sin=s_, chunk=chunk).float().cpu()
     for b, L in enumerate(lens):   # nothing written past each row's new token
         assert torch.all(kc[b, :, L:] == POISON) and torch.all(vc[b, :, L:] == POISON)
     qn = oracle.head_norm_rope(q, wq, 1e-6, cos, sin).float()       # [B, H, 1, D]
@@ -131,15 +131,18 @@ def test_c3_decode_full_size():
     _argmax_ok(got, ref)
 
 
-def test_c4_ragged_decode_full_size():
-    """C4 at the benchmark's workload: 64 rows, lengths U[1024, 32768] from seed 0 (up to 64
-    split-K chunks per row). The longest, the shortest and six sampled rows against the
+@pytest.mark.parametrize("chunk", [0, 512])
+def test_c4_ragged_decode_full_size(chunk):
+    """C4 at the benchmark's workload: 64 rows, lengths U[1024, 32768] from seed 0, with the
+    default chunk (1024 keys: up to 32 split-K chunks per row, as bench.py runs it) and with
+    512-key chunks (up to 64). The longest, the shortest and six sampled rows against the
     oracle; every row against an fp32 torch reference on the GPU over the cache as written."""
     g = torch.Generator().manual_seed(0)
     lens = torch.randint(1024, 32768 + 1, (64,), generator=g).tolist()    # bench.py c4_lengths(0)
     H, K, D = 16, 8, 128
-    got, kc, vc, qn, kappend, vn, sc = _decode_full(lens, H, K, D, 1e6, seed=0)
-    assert ops().decode_chunk(BF, 64, 1, H, K, D, max(lens)) * 63 < max(lens)   # >= 64 chunks
+    got, kc, vc, qn, kappend, vn, sc = _decode_full(lens, H, K, D, 1e6, seed=0, chunk=chunk)
+    used = chunk or ops().decode_chunk(BF, 64, 1, H, K, D, max(lens))
+    assert used * (31 if chunk == 0 else 63) < max(lens)   # >= 32 (64) chunks in the longest row
     order = sorted(range(64), key=lambda b: lens[b])
     pick = sorted({order[0], order[-1], *torch.randperm(64, generator=g)[:6].tolist()})
     ref = torch.cat([_oracle_row(b, lens[b], kc, vc, qn, kappend, vn, sc) for b in pick], 0)

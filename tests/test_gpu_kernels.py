@@ -245,6 +245,43 @@ def test_persistent_verify_row_blocks_with_early_returns(dtype):
         assert torch.equal(dense, persistent)
 
 
+@pytest.mark.parametrize("T,H,K", [(1, 16, 8), (2, 8, 8)])
+def test_persistent_runs_equal_per_row_dense_calls(T, H, K):
+    """Ragged rows on the persistent grid (64 rows, up to 47 chunks each, units taken by
+    ticket in any order) equal bit for bit the same rows computed one at a time on the dense
+    grid (T = 2: two query rows with different last keys in one row block)."""
+    g = gen(61)
+    B, D, chunk = 64, 128, 128
+    lens = torch.randint(T, 6000, (B,), generator=torch.Generator().manual_seed(61)).tolist()
+    L = max(lens)
+    kc = randn(g, B, K, L, D, dtype=torch.bfloat16).to(DEV)
+    vc = randn(g, B, K, L, D, dtype=torch.bfloat16).to(DEV)
+    q = randn(g, B, H, T, D, dtype=torch.bfloat16).to(DEV)
+    rp = torch.tensor([n - T for n in lens], dtype=torch.int32, device=DEV)
+    o = ops()
+    for _ in range(2):   # the second call reuses the first one's cleared work ticket
+        got = o.attn_decode(q, kc, vc, scale=0.1, row_pos=rp, max_kv_len=L, chunk=chunk)
+        for b in range(B):
+            want = o.attn_decode(q[b:b + 1], kc[b:b + 1], vc[b:b + 1], scale=0.1, pos=lens[b] - T, chunk=chunk)
+            assert torch.equal(got[b:b + 1], want), (b, lens[b])
+
+
+def test_decode_append_runs_equal_per_row_dense_calls():
+    """forge_attn_decode_append on ragged rows of the persistent grid (the unit holding a
+    row's last chunk also makes the new keys) equals the two calls, and each row equals its
+    own dense-grid decode over the cache the append wrote, bit for bit."""
+    lens = torch.randint(2, 5000, (64,), generator=torch.Generator().manual_seed(62)).tolist()
+    (y1, k1, v1), (y2, k2, v2), (q, k, v, wq, wk, c, s) = _append_decode_pair(
+        63, torch.bfloat16, 64, 16, 8, 128, 1, lens, 0, "row_pos", chunk=128)
+    assert torch.equal(y1, y2) and torch.equal(k1, k2) and torch.equal(v1, v2)
+    o = ops()
+    for b, n in enumerate(lens):
+        want = o.attn_decode(q[b:b + 1], k1[b:b + 1], v1[b:b + 1], scale=scale_of(128), pos=n - 1,
+                             q_weight=wq, eps=1e-6, norm_q=True, cos=c[b], sin=s[b], chunk=128,
+                             max_kv_len=n)
+        assert torch.equal(y2[b:b + 1], want), (b, n)
+
+
 # ------------------------------------------------------------------ MTP drafter attention
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("H,K,D", [(8, 2, 128), (8, 1, 256)])
