@@ -1362,27 +1362,41 @@ static int device_cus() {
   return ncu;
 }
 
+// MFMA verify path: the smallest multiple of 32 keys that puts every unit into one round of
+// the device's block slots (CUs x blocks per CU): with one more unit than slots, the last
+// few full units run as a second round and double the kernel's time. (rows of T = 1, as
+// the module asks.)
+static int verify_round_chunk(int B, int H, int K, int D, int64_t max_kv_len) {
+  const int T = 1;
+  const int G = H / K;
+  const int64_t pairs = (int64_t)B * K * ((G * T + kVerifyRows - 1) / kVerifyRows);
+  const int64_t len = max_kv_len > 0 ? max_kv_len : 1;
+  const int64_t slots = (int64_t)verify_blocks_per_cu(D) * device_cus();
+  const int64_t per_pair = slots / pairs > 1 ? slots / pairs : 1;  // chunks per (b, kv head, rows)
+  int64_t chunk = (len + per_pair - 1) / per_pair;
+  chunk = (chunk + 31) / 32 * 32;
+  // At least as many tiles as the pipeline keeps in flight: a shorter unit cannot use its
+  // prefetch and is mostly prologue (C5 window 1024: 64-key chunks 23.2 us, 96-key 20.9 us).
+  constexpr int kMinTiles = VerifyTile<128>::STAGES - 1;
+  static_assert(VerifyTile<128>::STAGES == VerifyTile<256>::STAGES &&
+                VerifyTile<128>::BN == VerifyTile<256>::BN, "one tile shape for both head dims");
+  const int64_t min_chunk = (int64_t)kMinTiles * VerifyTile<128>::BN;
+  return (int)(chunk < min_chunk ? min_chunk : chunk);
+}
+
+// Longest chunk of the MFMA verify path for device-held or per-row positions: a ragged
+// batch's long rows would otherwise be few long units that finish last (C4 lengths at
+// 32 q / 8 KV heads: 1012 us per decode step at 512-key chunks against 1205 us for one chunk
+// per row; 28 q / 4 KV heads, 32 rows: 208 against 304 us; 8 q / 1 KV head, T = 4, 32 rows:
+// 72 against 90 us; 256-key chunks were as fast or slower, 1024 slower for all three).
+constexpr int kMaxVerifyChunk = 512;
+
 static int auto_chunk(int dtype, int B, int /*T*/, int H, int K, int D, int64_t max_kv_len) {
   const int T = 1;
   const int G = H / K;
   if (use_verify_mfma(dtype, D, G)) {
-    // The smallest multiple of 32 keys that puts every unit into one round of the device's
-    // block slots (CUs x blocks per CU): with one more unit than slots, the last few full
-    // units run as a second round and double the kernel's time. (rows of T = 1, as the
-    // module asks.)
-    const int64_t pairs = (int64_t)B * K * ((G * T + kVerifyRows - 1) / kVerifyRows);
-    const int64_t len = max_kv_len > 0 ? max_kv_len : 1;
-    const int64_t slots = (int64_t)verify_blocks_per_cu(D) * device_cus();
-    const int64_t per_pair = slots / pairs > 1 ? slots / pairs : 1;  // chunks per (b, kv head, rows)
-    int64_t chunk = (len + per_pair - 1) / per_pair;
-    chunk = (chunk + 31) / 32 * 32;
-    // At least as many tiles as the pipeline keeps in flight: a shorter unit cannot use its
-    // prefetch and is mostly prologue (C5 window 1024: 64-key chunks 23.2 us, 96-key 20.9 us).
-    constexpr int kMinTiles = VerifyTile<128>::STAGES - 1;
-    static_assert(VerifyTile<128>::STAGES == VerifyTile<256>::STAGES &&
-                  VerifyTile<128>::BN == VerifyTile<256>::BN, "one tile shape for both head dims");
-    const int64_t min_chunk = (int64_t)kMinTiles * VerifyTile<128>::BN;
-    return (int)(chunk < min_chunk ? min_chunk : chunk);
+    const int chunk = verify_round_chunk(B, H, K, D, max_kv_len);
+    return chunk < kMaxVerifyChunk ? chunk : kMaxVerifyChunk;
   }
   const int rows = rows_per_block(G * T);
   const int64_t n_rb = (G * T + rows - 1) / rows;
@@ -1412,7 +1426,7 @@ static int auto_chunk(int dtype, int B, int /*T*/, int H, int K, int D, int64_t 
 // ignores T. The MFMA verify path keeps its own rule.
 static int uniform_chunk(int dtype, int B, int H, int K, int D, int64_t max_kv_len) {
   const int G = H / K;
-  if (use_verify_mfma(dtype, D, G)) return auto_chunk(dtype, B, 1, H, K, D, max_kv_len);
+  if (use_verify_mfma(dtype, D, G)) return verify_round_chunk(B, H, K, D, max_kv_len);
   const int rows = rows_per_block(G);
   const int64_t pairs = (int64_t)B * K * ((G + rows - 1) / rows);
   const int kpi = keys_per_iter(dtype, D);
