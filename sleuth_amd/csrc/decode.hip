@@ -1444,6 +1444,11 @@ static int uniform_chunk(int dtype, int B, int H, int K, int D, int64_t max_kv_l
       best_cost = cost;
     }
   }
+  // With fewer pairs than CUs every row must be split to fill them. The span is a cache's
+  // capacity, which a row may be far from reaching, so the chunk stays at most as long as
+  // the general rule's (a capacity of 32768 at C2's 64 pairs would otherwise give 8192-key
+  // chunks, one unit per row of 2049 keys: 30.9 us per call against 19.9 us).
+  if (pairs < ncu && best > kMaxChunk) best = kMaxChunk;
   return best > INT_MAX ? INT_MAX / kpi * kpi : (int)best;
 }
 

@@ -60,7 +60,8 @@ def test_uniform_chunk_rule():
     assert ch(32, 16, 8, 128, 8192) == 8192      # C3 decode: 256 pairs, one unit per CU
     assert ch(64, 16, 8, 128, 4096) == 4096      # 512 pairs: two per CU, still no split
     assert ch(48, 16, 8, 128, 8192) == 4096      # 384 pairs: 768 units = 3 per CU
-    assert ch(24, 16, 8, 128, 8192) == 2048      # 192 pairs: 768 units
+    assert ch(24, 16, 8, 128, 8192) == 1024      # 192 pairs: the rule's 2048, at most 1024 below 256 pairs
+    assert ch(16, 12, 4, 64, 32768) == 1024      # C2's pairs at a large capacity: rows stay split
     assert ch(16, 12, 4, 64, 2049) == 576        # C2: 64 pairs x 4 chunks = 256 units
     assert ch(1, 8, 4, 64, 50) == 64             # one short row: one chunk of one iteration
     for B, H, K, D, L in [(32, 16, 8, 128, 8192), (16, 12, 4, 64, 2049), (3, 8, 2, 32, 777),
