@@ -1426,7 +1426,15 @@ static int auto_chunk(int dtype, int B, int /*T*/, int H, int K, int D, int64_t 
 // ignores T. The MFMA verify path keeps its own rule.
 static int uniform_chunk(int dtype, int B, int H, int K, int D, int64_t max_kv_len) {
   const int G = H / K;
-  if (use_verify_mfma(dtype, D, G)) return verify_round_chunk(B, H, K, D, max_kv_len);
+  if (use_verify_mfma(dtype, D, G)) {
+    // rows split four ways or more: as below, a capacity far above the rows' length must
+    // not leave one long unit per row (C5's 8 rows in caches of 131072 would get 4096-key
+    // chunks, 24 units)
+    const int chunk = verify_round_chunk(B, H, K, D, max_kv_len);
+    const int64_t pairs = (int64_t)B * K * ((G + kVerifyRows - 1) / kVerifyRows);
+    const bool split = pairs * 4 <= (int64_t)verify_blocks_per_cu(D) * device_cus();
+    return split && chunk > kMaxVerifyChunk ? kMaxVerifyChunk : chunk;
+  }
   const int rows = rows_per_block(G);
   const int64_t pairs = (int64_t)B * K * ((G + rows - 1) / rows);
   const int kpi = keys_per_iter(dtype, D);

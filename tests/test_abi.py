@@ -69,8 +69,10 @@ def test_uniform_chunk_rule():
         c = ch(B, H, K, D, L)
         kpi = (256 // (D // 8)) * 2
         assert c % kpi == 0 and c >= min(4 * kpi, -(-L // kpi) * kpi)
-    # the MFMA verify shapes (G >= 4, hd 128/256, bf16/fp16) keep their own rule
-    assert ch(8, 8, 1, 256, 8196) == lib.forge_attn_decode_chunk(_lib.BF16, 8, 1, 8, 1, 256, 8196)
+    # the MFMA verify shapes (G >= 4, hd 128/256, bf16/fp16): one round of block slots
+    assert ch(8, 8, 1, 256, 8196) == 288 == lib.forge_attn_decode_chunk(_lib.BF16, 8, 1, 8, 1, 256, 8196)
+    assert ch(32, 32, 8, 128, 8192) == 4096      # 256 pairs, 512 slots: two chunks per row
+    assert ch(8, 8, 1, 256, 131072) == 512       # split rows of a large capacity: at most 512 keys
     assert ch(1, 8, 3, 64, 100) == 0             # H % K != 0
 
 
