@@ -700,7 +700,7 @@ void splitk_kernel(SplitParams p) {
     const int r0 = tid * seg;
     const int r1 = r0 + seg < p.B ? r0 + seg : p.B;
     int sum = 0;
-    for (int r = r0; r < r1; ++r) sum += sh_nch[r] * per_row;
+    for (int r = r0; r < r1; ++r) sum += (sh_nch[r] > 0 ? sh_nch[r] - 1 : 0) * per_row;
     int incl = sum;
 #pragma unroll
     for (int d = 1; d < kWave; d <<= 1) {
@@ -710,12 +710,19 @@ void splitk_kernel(SplitParams p) {
     int run = incl - sum;
     for (int r = r0; r < r1; ++r) {
       sh_pref[r] = run;
-      run += sh_nch[r] * per_row;
+      run += (sh_nch[r] > 0 ? sh_nch[r] - 1 : 0) * per_row;
     }
     if (tid == kWave - 1) sh_pref[p.B] = incl;
   }
   __syncthreads();
-  const int total = sh_pref[p.B];
+  // Units [0, body) are every row's chunks but its last, (row, KV head x row block, chunk)
+  // with the chunk fastest, each row's from its second-to-last chunk down; units
+  // [body, total) are the rows' last chunks, (row, KV head x row block). A ragged batch's
+  // last chunks are partial (a random part of a chunk each), so handing them out last
+  // shortens the units left when blocks run out of work (C4 step 607.9 us against 609.7 us
+  // with each row's last chunk first, same box).
+  const int body = sh_pref[p.B];
+  const int total = body + p.B * per_row;
   // Block i starts with unit i; after that units go by ticket (grid + an atomic counter
   // in the workspace, which the host zeroes before the launch), so a block on a CU that
   // streams faster takes more of them. A block fetches its next ticket when it starts a
@@ -730,21 +737,32 @@ void splitk_kernel(SplitParams p) {
   // coordinates, and the cache slab's buffer descriptors built from them, in scalar
   // registers.)
   for (int u = blockIdx.x; u < total; u = __builtin_amdgcn_readfirstlane(sh_ticket[parity]), parity ^= 1) {
-    int next = 0;              // split_unit sets it on every path
-    int lo = 0, hi = p.B - 1;  // last row with sh_pref[row] <= u
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (__builtin_amdgcn_readfirstlane(sh_pref[mid]) <= u) lo = mid;
-      else hi = mid - 1;
+    int next = 0;  // split_unit sets it on every path
+    int lo, pr, cidx;  // row, (KV head, row block), chunk counted from the row's first
+    if (u < body) {
+      lo = 0;
+      int hi = p.B - 1;  // last row with sh_pref[row] <= u
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (__builtin_amdgcn_readfirstlane(sh_pref[mid]) <= u) lo = mid;
+        else hi = mid - 1;
+      }
+      const int o = u - __builtin_amdgcn_readfirstlane(sh_pref[lo]);
+      const int n = __builtin_amdgcn_readfirstlane(sh_nch[lo]) - 1;  // >= 1 here
+      pr = o / n;
+      cidx = n - 1 - o % n;
+    } else {
+      // a row with no visible key has no last chunk either: cidx -1 lies before every key,
+      // and the unit returns at once
+      const int q = u - body;
+      lo = q / per_row;
+      pr = q % per_row;
+      cidx = __builtin_amdgcn_readfirstlane(sh_nch[lo]) - 1;
     }
-    const int o = u - __builtin_amdgcn_readfirstlane(sh_pref[lo]);
-    const int n = __builtin_amdgcn_readfirstlane(sh_nch[lo]);
-    const int pr = o / n;
     const int base = __builtin_amdgcn_readfirstlane(sh_base[lo]);
     int kmin, kmax;
     visible_range32(base, p.window, (int)p.max_len, kmin, kmax);  // the row's first chunk
-    // a row's chunks last to first (the last one's unit also makes the new keys)
-    split_unit<T, D, ROWS>(p, lo, base, pr % p.K, pr / p.K, kmin / p.chunk + (n - 1 - o % n), sh, &next);
+    split_unit<T, D, ROWS>(p, lo, base, pr % p.K, pr / p.K, kmin / p.chunk + cidx, sh, &next);
     if (tid == 0) sh_ticket[parity] = (int)gridDim.x + next;
     __syncthreads();  // the next unit reuses the merge LDS; the ticket is visible
   }
