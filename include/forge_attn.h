@@ -195,6 +195,22 @@ int forge_attn_prefill(int dtype, int B, int T, int H, int K, int D, const void*
                        int64_t skh, int64_t sks, int64_t offset, int window, float scale,
                        void* out, int64_t sob, int64_t sot, int64_t soh, void* stream);
 
+/*
+ * forge_attn_prefill with document masking: the reference's `same_doc` mask, causal and only
+ * within a document (transformer.py:271-275 builds it from doc_ids, attention.py:184-186
+ * applies it), for forward passes over packed windows such as scoring. doc_start[b * s_doc_b
+ * + t] is the position of the first token of query t's document; the documents of a row are
+ * contiguous runs, so doc_start is non-decreasing in t and doc_start <= offset + t (the
+ * caller checks both). Query t then sees keys [max(doc_start, window bound), offset + t].
+ */
+int forge_attn_prefill_docs(int dtype, int B, int T, int H, int K, int D, const void* q,
+                            int64_t sqb, int64_t sqh, int64_t sqt, const float* q_weight,
+                            float eps, int flags, const float* cos, const float* sin,
+                            int64_t s_cos_t, const void* k, const void* v, int64_t skb,
+                            int64_t skh, int64_t sks, int64_t offset, int window, float scale,
+                            const int32_t* doc_start, int64_t s_doc_b, void* out, int64_t sob,
+                            int64_t sot, int64_t soh, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

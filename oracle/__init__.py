@@ -12,6 +12,7 @@ from .attention_ref import (  # noqa: F401
     attention_forward,
     attention_mask,
     brute_attention,
+    document_mask,
     eager_norm_rope,
     drafter_attention,
     explicit_attention,

@@ -13,6 +13,8 @@ Parity pins (tests/test_oracle.py), chosen so that a plausible slip fails one of
   sdpa / explicit_attention  float64 brute force with explicit loops and the GQA map
                              kv = h // (H/K) (brute_attention); single-key and equal-key
                              closed forms; causality
+  document_mask / sdpa with  the loops restricted to the query's document; a packed window
+    same_doc                 equals each document attended alone
   gated_attention            float64 loops from the definition (partial RoPE on the first
                              n_rot channels, q | gate split per head, sigmoid gate, causal
                              at an offset), tests/test_oracle.py
@@ -108,14 +110,27 @@ def attention_mask(T: int, S: int, offset: int, window: int = 0) -> torch.Tensor
     return mask
 
 
+def document_mask(doc_ids: torch.Tensor) -> torch.Tensor:
+    """Transformer.forward's document mask (transformer.py:271-275): doc_ids [B, T] ->
+    same_doc [B, 1, T, T] bool, True where query and key belong to one document."""
+    return (doc_ids[:, :, None] == doc_ids[:, None, :])[:, None]
+
+
 # ----------------------------------------------------------------------------- attention
 def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, offset: int, window: int,
-         scale: float) -> torch.Tensor:
+         scale: float, same_doc: torch.Tensor | None = None) -> torch.Tensor:
     """Attention._fused (attention.py:171-193) with enable_gqa: q [B,H,T,hd], k/v
-    [B,K,S,hd] -> [B,H,T,hd]. Same dispatch: is_causal when offset == 0 and not
-    windowed, no mask when T == 1 and not windowed, else the boolean _mask."""
+    [B,K,S,hd] -> [B,H,T,hd]. Same dispatch: with a document mask same_doc [B,1,T,S],
+    K/V heads repeated and _mask & same_doc (attention.py:177-186); else is_causal when
+    offset == 0 and not windowed, no mask when T == 1 and not windowed, else the boolean
+    _mask."""
     T, S = q.shape[2], k.shape[2]
     kw = {"scale": scale}
+    if same_doc is not None:
+        rep = q.shape[1] // k.shape[1]
+        k, v = k.repeat_interleave(rep, dim=1), v.repeat_interleave(rep, dim=1)
+        mask = attention_mask(T, S, offset, window).to(q.device) & same_doc
+        return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, **kw)
     if k.shape[1] != q.shape[1]:
         kw["enable_gqa"] = True
     windowed = bool(window) and S > window
@@ -143,10 +158,12 @@ def explicit_attention(q, k, v, offset: int, window: int, scale: float,
     return (out, probs) if return_probs else out
 
 
-def brute_attention(q, k, v, offset: int, window: int, scale: float) -> torch.Tensor:
+def brute_attention(q, k, v, offset: int, window: int, scale: float,
+                    doc_ids: torch.Tensor | None = None) -> torch.Tensor:
     """Independent float64 restatement with explicit loops (small inputs only): for each
     batch row b, head h (KV head h // (H/K)) and query i at position offset + i, a
-    softmax over the keys j with j <= pos and pos - j < window. Returns float64."""
+    softmax over the keys j with j <= pos and pos - j < window (and, with doc_ids [B, S]
+    of the key positions, doc_ids[b, j] == doc_ids[b, pos]). Returns float64."""
     B, H, T, D = q.shape
     K, S = k.shape[1], k.shape[2]
     G = H // K
@@ -157,7 +174,8 @@ def brute_attention(q, k, v, offset: int, window: int, scale: float) -> torch.Te
             kvh = h // G
             for i in range(T):
                 pos = offset + i
-                js = [j for j in range(S) if j <= pos and (not window or pos - j < window)]
+                js = [j for j in range(S) if j <= pos and (not window or pos - j < window)
+                      and (doc_ids is None or int(doc_ids[b, j]) == int(doc_ids[b, pos]))]
                 s = [float((qd[b, h, i] * kd[b, kvh, j]).sum()) * scale for j in js]
                 mx = max(s)
                 w = [math.exp(x - mx) for x in s]
@@ -262,7 +280,7 @@ class StaticKVCache(KVCache):
 # ----------------------------------------------------------------------------- one layer
 def attention_forward(q, k, v, *, cos, sin, scale, eps=1e-6, q_weight=None, k_weight=None,
                       qk_norm=True, v_norm=False, use_rope=True, window=0, cache=None, layer=0,
-                      fused_norm=True):
+                      fused_norm=True, same_doc=None):
     """Attention.forward after the projections (attention.py:109-153): q [B,H,T,hd],
     k/v [B,K,T,hd] raw projections -> y [B,H,T,hd]. fused_norm=True follows the GPU
     inference path (head_norm_rope, one rounding, attention.py:109-119), False the eager
@@ -287,7 +305,7 @@ def attention_forward(q, k, v, *, cos, sin, scale, eps=1e-6, q_weight=None, k_we
     if getattr(cache, "static", False):
         kw = {"enable_gqa": True} if k.shape[1] != q.shape[1] else {}
         return F.scaled_dot_product_attention(q, k, v, attn_mask=cache.attn_mask(window), scale=scale, **kw)
-    return sdpa(q, k, v, S - T, window, scale)
+    return sdpa(q, k, v, S - T, window, scale, same_doc)
 
 
 # ----------------------------------------------------------------------------- gated attention

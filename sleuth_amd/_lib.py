@@ -90,6 +90,16 @@ SIGNATURES: dict[str, tuple] = {
         _i64, _i, _f,                        # offset, window, scale
         _p, _i64, _i64, _i64,                # out + strides (b, t, h)
         _p]),
+    "forge_attn_prefill_docs": (_i, [
+        _i, _i, _i, _i, _i, _i,              # dtype, B, T, H, K, D
+        _p, _i64, _i64, _i64,                # q + strides
+        _p, _f, _i,                          # q_weight, eps, flags
+        _p, _p, _i64,                        # cos, sin, s_cos_t
+        _p, _p, _i64, _i64, _i64,            # k, v, skb, skh, sks
+        _i64, _i, _f,                        # offset, window, scale
+        _p, _i64,                            # doc_start, its row stride
+        _p, _i64, _i64, _i64,                # out + strides (b, t, h)
+        _p]),
 }
 
 _lock = threading.Lock()

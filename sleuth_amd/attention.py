@@ -7,8 +7,8 @@ signature forward(x, cos, sin, cache=None, same_doc=None) -> [B, T, d].
 
 Paths (the reference's own dispatch, attention.py:109-153, with the HIP kernels in place
 of head_norm_rope + cache.update + SDPA):
-  * HIP (GPU inference: no grad, dtype fp32/bf16/fp16, head dim 32/64/128/256, no
-    document mask, nobody listening on attn.pattern):
+  * HIP (GPU inference: no grad, dtype fp32/bf16/fp16, head dim 32/64/128/256, nobody
+    listening on attn.pattern; a document mask only as below):
       k norm + RoPE (+ v norm), written into the cache at pos / pos_t / per-row
       lengths (with partial RoPE, norm and RoPE run in torch as the reference's eager
       code does, and the kernels take q and k as they are), then attention:
@@ -17,9 +17,12 @@ of head_norm_rope + cache.update + SDPA):
       otherwise         forge_attn_decode_append: the cache write and the split-K
                         attention (decode, verify, static steps, fp32, other head sizes)
                         in one launch, the q norm + RoPE fused into the q load.
+      A boolean document mask (transformer.py:271-275) over a whole window (no cache,
+      T > 16, the prefill dtypes and head dims) whose documents are contiguous runs goes
+      to forge_attn_prefill_docs, which takes each query's first visible key.
     The output comes back as [B, T, H, hd], the layout o_proj reads.
-  * torch (CPU, training, document masks, the pattern tap, or
-    SLEUTH_AMD_NO_HIP=1): the reference's eager code, unchanged in meaning.
+  * torch (CPU, training, FlexAttention block masks and other document masks, the
+    pattern tap, or SLEUTH_AMD_NO_HIP=1): the reference's eager code, unchanged in meaning.
 If a GPU tensor would take the HIP path and the library is missing or fails its
 first-use self-check, forward raises: there is no silent fallback.
 """
@@ -47,6 +50,32 @@ _checked: dict[tuple, bool] = {}
 
 def hip_disabled() -> bool:
     return os.environ.get("SLEUTH_AMD_NO_HIP") == "1"
+
+
+_DOC_STARTS: dict = {}   # the last mask's doc starts: one mask serves every layer of a pass
+
+
+def _doc_starts(same_doc, B: int, T: int) -> torch.Tensor | None:
+    """The reference's document mask (transformer.py:271-275: [B or 1, 1, T, T] bool, True
+    where query and key are in one document) as each query's first visible key, [B, T]
+    int32, for forge_attn_prefill_docs. None where it is not such a mask, or where a query's
+    visible keys (mask and causal) are not one run ending at the query itself, i.e. its
+    document is not a contiguous run of positions."""
+    m = same_doc
+    if not (isinstance(m, torch.Tensor) and m.dtype == torch.bool and m.is_cuda and m.dim() == 4
+            and m.shape[1] == 1 and tuple(m.shape[2:]) == (T, T) and m.shape[0] in (1, B)):
+        return None
+    hit = _DOC_STARTS.get("last")
+    if hit is not None and hit[0]() is m and hit[1] == (m._version, B):
+        return hit[2]
+    vis = m[:, 0] & torch.ones(T, T, dtype=torch.bool, device=m.device).tril()
+    start = vis.to(torch.int32).argmax(-1)                  # the first visible key
+    pos = torch.arange(T, device=m.device)
+    run = (vis.sum(-1) == pos - start + 1).all() & vis.diagonal(dim1=-2, dim2=-1).all()
+    run &= (start[:, 1:] >= start[:, :-1]).all()
+    res = start.to(torch.int32).expand(B, T).contiguous() if bool(run) else None
+    _DOC_STARTS["last"] = (weakref.ref(m), (m._version, B), res)
+    return res
 
 
 def _hip_ready(device: torch.device, dtype: torch.dtype) -> None:
@@ -161,19 +190,30 @@ class Attention(nn.Module):
         return F.linear(x, w, b)
 
     # ------------------------------------------------------------------ dispatch
-    def _use_hip(self, q: torch.Tensor, cache, same_doc) -> bool:
+    def _use_hip(self, q: torch.Tensor, cache, same_doc) -> tuple[bool, torch.Tensor | None]:
+        """(take the HIP path, the document starts of a document mask or None)"""
         if not q.is_cuda or hip_disabled():
-            return False
+            return False, None
         if torch.is_grad_enabled() and q.requires_grad:
-            return False
-        if same_doc is not None or tap_active(self.tap_pattern):
-            return False
+            return False, None
+        if tap_active(self.tap_pattern):
+            return False, None
         if q.dtype not in _HIP_DTYPES or self.hd not in _HIP_HEAD_DIMS:
-            return False
+            return False, None
         if cache is not None and cache.k[self.layer_idx].dtype != q.dtype:
-            return False   # the reference's SDPA needs q and the cache in one dtype too
+            return False, None   # the reference's SDPA needs q and the cache in one dtype too
+        docs = None
+        if same_doc is not None:
+            from . import ops
+
+            if cache is not None or q.shape[2] <= DECODE_MAX_T or not ops.prefill_supported(q) or \
+                    torch.cuda.is_current_stream_capturing():
+                return False, None
+            docs = _doc_starts(same_doc, q.shape[0], q.shape[2])
+            if docs is None:
+                return False, None
         _hip_ready(q.device, q.dtype)
-        return True
+        return True, docs
 
     def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, cache=None,
                 same_doc=None) -> torch.Tensor:
@@ -188,8 +228,9 @@ class Attention(nn.Module):
             q = self.q_proj(x).view(B, T, H, hd).transpose(1, 2)  # [B, H, T, hd]
             k = self.k_proj(x).view(B, T, K, hd).transpose(1, 2)  # [B, K, T, hd]
             v = k if self.v_proj is None else self.v_proj(x).view(B, T, K, hd).transpose(1, 2)
-        if self._use_hip(q, cache, same_doc):
-            y = self._forward_hip(q, k, v, cos, sin, cache)
+        hip, docs = self._use_hip(q, cache, same_doc)
+        if hip:
+            y = self._forward_hip(q, k, v, cos, sin, cache, docs)
         else:
             y = self._forward_torch(q, k, v, cos, sin, cache, same_doc).transpose(1, 2)
             self.last_path = "torch"
@@ -197,7 +238,7 @@ class Attention(nn.Module):
         return self.o_proj(y.reshape(B, T, self.n_heads * self.hd))
 
     # ------------------------------------------------------------------ HIP path
-    def _forward_hip(self, q, k, v, cos, sin, cache) -> torch.Tensor:
+    def _forward_hip(self, q, k, v, cos, sin, cache, docs=None) -> torch.Tensor:
         from . import ops
 
         B, H, T, hd = q.shape
@@ -263,8 +304,11 @@ class Attention(nn.Module):
         if T > DECODE_MAX_T and offset is not None and ops.prefill_supported(q) and \
                 (q_args["cos"] is None or q_args["cos"].dim() == 2):
             ops.kv_append(k, v, kc, vc, norm_v=norm_v, **pos_kw, **k_args)
-            self.last_path = "hip-prefill"
-            return ops.attn_prefill(q, kc, vc, scale=self.scale, offset=offset, window=self.window, **q_args)
+            self.last_path = "hip-prefill" if docs is None else "hip-prefill-docs"
+            return ops.attn_prefill(q, kc, vc, scale=self.scale, offset=offset, window=self.window,
+                                    doc_start=docs, **q_args)
+        if docs is not None:
+            raise RuntimeError("a document mask needs the prefill path (no cache, T > 16)")
         # the cache write and the attention in one call (one launch where the shape allows);
         # q and k share the RoPE tables and the eps (both come from this module's config)
         self.last_path = "hip-decode"

@@ -74,6 +74,10 @@ struct PrefillParams {
   float scale_log2;
   void* out;
   int64_t sob, sot, soh;
+  // Document masking (forge_attn_prefill_docs): query t of row b also sees no key before
+  // position doc_lo[b * sdb + t], the first of its document (non-decreasing in t); or null.
+  const int32_t* doc_lo;
+  int64_t sdb;
 };
 
 constexpr float kLazyLog2 = 8.0f;
@@ -171,6 +175,12 @@ void prefill_kernel(PrefillParams p) {
   const int64_t blk_kmax = p.offset + q_last_idx;
   int64_t blk_kmin = p.window > 0 ? q_first - p.window + 1 : 0;
   if (blk_kmin < 0) blk_kmin = 0;
+  // with documents: the block's first query starts the earliest document of the block
+  const int32_t* dl = p.doc_lo ? p.doc_lo + b * p.sdb : nullptr;
+  if (dl) {
+    const int64_t d0 = __builtin_amdgcn_readfirstlane(dl[(int64_t)qt * kBM]);
+    if (d0 > blk_kmin) blk_kmin = d0;
+  }
   const int kt_begin = (int)(blk_kmin / BN);
   const int kt_end = (int)(blk_kmax / BN);
 
@@ -294,6 +304,14 @@ void prefill_kernel(PrefillParams p) {
   const int wq_lo = off + w_first, wq_hi = off + w_last;
   const int S32 = (int)S;
   const int qpos32 = (int)qpos;
+  // document starts: this lane's query's, and the first (smallest) and last (largest) of the
+  // wave's queries (loads of rows past T read row T - 1; those lanes are masked anyway)
+  int d_lane = 0, d_wfirst = 0, d_wlast = 0;
+  if (dl) {
+    d_lane = dl[i_q < p.T ? i_q : p.T - 1];
+    d_wfirst = __builtin_amdgcn_readfirstlane(d_lane);
+    d_wlast = __builtin_amdgcn_readlane(d_lane, w_last - w_first > 0 ? w_last - w_first : 0);
+  }
 
   // LDS read offsets (bytes within a stage buffer).
   // K operand: row 32kb + n, chunk 2s + hi, swizzled by row & 15 == n & 15.
@@ -326,10 +344,12 @@ void prefill_kernel(PrefillParams p) {
 
     const int key0 = kt * BN;
     const bool wave_needs = wave_any && key0 <= wq_hi &&
-                            (p.window <= 0 || key0 + BN - 1 > wq_lo - p.window);
+                            (p.window <= 0 || key0 + BN - 1 > wq_lo - p.window) &&
+                            key0 + BN - 1 >= d_wfirst;
     if (!wave_needs) continue;
     const bool full = key0 + BN - 1 <= wq_lo && key0 + BN - 1 < S32 &&
-                      (p.window <= 0 || wq_hi - key0 < p.window) && w_last - w_first == 31;
+                      (p.window <= 0 || wq_hi - key0 < p.window) && w_last - w_first == 31 &&
+                      key0 >= d_wlast;
 
     const char* kl = smem + (2 * stage) * TL::TILEB + k_rd;
     const char* vl = smem + (2 * stage + 1) * TL::TILEB;
@@ -377,7 +397,8 @@ void prefill_kernel(PrefillParams p) {
       const int base = key0 + 4 * hi;
       const int top = (qpos32 < S32 - 1 ? qpos32 : S32 - 1) - base;
       const int lim_hi = valid_q ? top : -1;
-      const int lim_lo = p.window > 0 ? qpos32 - p.window + 1 - base : -(1 << 30);
+      int lim_lo = p.window > 0 ? qpos32 - p.window + 1 - base : -(1 << 30);
+      if (dl && d_lane - base > lim_lo) lim_lo = d_lane - base;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -489,14 +510,12 @@ static int launch_prefill(const PrefillParams& p, int D, hipStream_t s) {
 
 using namespace forge;
 
-extern "C" int forge_attn_prefill(int dtype, int B, int T, int H, int K, int D, const void* q,
-                                  int64_t sqb, int64_t sqh, int64_t sqt, const float* q_weight,
-                                  float eps, int flags, const float* cos, const float* sin,
-                                  int64_t s_cos_t, const void* k, const void* v, int64_t skb,
-                                  int64_t skh, int64_t sks, int64_t offset, int window,
-                                  float scale, void* out, int64_t sob, int64_t sot, int64_t soh,
-                                  void* stream) {
-  clear_error();
+static int prefill_call(int dtype, int B, int T, int H, int K, int D, const void* q, int64_t sqb,
+                        int64_t sqh, int64_t sqt, const float* q_weight, float eps, int flags,
+                        const float* cos, const float* sin, int64_t s_cos_t, const void* k,
+                        const void* v, int64_t skb, int64_t skh, int64_t sks, int64_t offset,
+                        int window, float scale, void* out, int64_t sob, int64_t sot, int64_t soh,
+                        const int32_t* doc_lo, int64_t sdb, void* stream) {
   if (dtype != FORGE_BF16 && dtype != FORGE_F16)
     return set_error("forge_attn_prefill: dtype must be bf16 or fp16 (use forge_attn_decode)");
   if (D != 64 && D != 128 && D != 256)
@@ -545,6 +564,37 @@ extern "C" int forge_attn_prefill(int dtype, int B, int T, int H, int K, int D, 
   p.sob = sob;
   p.sot = sot;
   p.soh = soh;
+  p.doc_lo = doc_lo;
+  p.sdb = sdb;
   hipStream_t s = (hipStream_t)stream;
   return dtype == FORGE_BF16 ? launch_prefill<bf16>(p, D, s) : launch_prefill<f16>(p, D, s);
+}
+
+extern "C" int forge_attn_prefill(int dtype, int B, int T, int H, int K, int D, const void* q,
+                                  int64_t sqb, int64_t sqh, int64_t sqt, const float* q_weight,
+                                  float eps, int flags, const float* cos, const float* sin,
+                                  int64_t s_cos_t, const void* k, const void* v, int64_t skb,
+                                  int64_t skh, int64_t sks, int64_t offset, int window,
+                                  float scale, void* out, int64_t sob, int64_t sot, int64_t soh,
+                                  void* stream) {
+  clear_error();
+  return prefill_call(dtype, B, T, H, K, D, q, sqb, sqh, sqt, q_weight, eps, flags, cos, sin,
+                      s_cos_t, k, v, skb, skh, sks, offset, window, scale, out, sob, sot, soh,
+                      nullptr, 0, stream);
+}
+
+extern "C" int forge_attn_prefill_docs(int dtype, int B, int T, int H, int K, int D,
+                                       const void* q, int64_t sqb, int64_t sqh, int64_t sqt,
+                                       const float* q_weight, float eps, int flags,
+                                       const float* cos, const float* sin, int64_t s_cos_t,
+                                       const void* k, const void* v, int64_t skb, int64_t skh,
+                                       int64_t sks, int64_t offset, int window, float scale,
+                                       const int32_t* doc_start, int64_t s_doc_b, void* out,
+                                       int64_t sob, int64_t sot, int64_t soh, void* stream) {
+  clear_error();
+  if (!doc_start) return set_error("forge_attn_prefill_docs: doc_start is null");
+  if ((uintptr_t)doc_start % 4) return set_error("forge_attn_prefill_docs: doc_start must be 4-byte aligned");
+  return prefill_call(dtype, B, T, H, K, D, q, sqb, sqh, sqt, q_weight, eps, flags, cos, sin,
+                      s_cos_t, k, v, skb, skh, sks, offset, window, scale, out, sob, sot, soh,
+                      doc_start, s_doc_b, stream);
 }

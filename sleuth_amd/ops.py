@@ -353,9 +353,15 @@ def prefill_supported(q: torch.Tensor) -> bool:
 def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float, offset: int = 0,
                  window: int = 0, q_weight: torch.Tensor | None = None, eps: float = 1e-6,
                  norm_q: bool = False, cos: torch.Tensor | None = None,
-                 sin: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                 sin: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                 doc_start: torch.Tensor | None = None) -> torch.Tensor:
     """Causal flash attention on MFMA: queries at positions offset..offset+T-1 over keys
-    0..offset+T-1 of k/v [B,K,>=offset+T,D]. Returns [B,T,H,D]."""
+    0..offset+T-1 of k/v [B,K,>=offset+T,D]. Returns [B,T,H,D].
+
+    doc_start: [B, T] int32, the position of the first token of each query's document (the
+    reference's document mask, transformer.py:271-275): query t also sees no key before it.
+    It must be non-decreasing along T and at most the query's own position (checked, except
+    under graph capture)."""
     B, H, T, D = q.shape
     Bk, K, S, Dk = k.shape
     if Bk != B or Dk != D or v.shape != k.shape or H % K:
@@ -378,12 +384,30 @@ def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: fl
         out = torch.empty(B, T, H, D, dtype=q.dtype, device=dev)
     elif out.shape != (B, T, H, D) or out.dtype != q.dtype:
         raise ValueError(f"out must be [B,T,H,D] = {(B, T, H, D)} {q.dtype}")
-    st = lib().forge_attn_prefill(dtype_code(q), B, T, H, K, D, _ptr(q), q.stride(0), q.stride(1),
-                                  q.stride(2), _ptr(w), float(eps), flags, _ptr(c), _ptr(s), s_t,
-                                  _ptr(k), _ptr(v), k.stride(0), k.stride(1), k.stride(2),
-                                  int(offset), int(window), float(scale),
-                                  _ptr(out), out.stride(0), out.stride(1), out.stride(2), _stream(dev))
-    check(st, "forge_attn_prefill")
+    if doc_start is None:
+        st = lib().forge_attn_prefill(dtype_code(q), B, T, H, K, D, _ptr(q), q.stride(0), q.stride(1),
+                                      q.stride(2), _ptr(w), float(eps), flags, _ptr(c), _ptr(s), s_t,
+                                      _ptr(k), _ptr(v), k.stride(0), k.stride(1), k.stride(2),
+                                      int(offset), int(window), float(scale),
+                                      _ptr(out), out.stride(0), out.stride(1), out.stride(2), _stream(dev))
+        check(st, "forge_attn_prefill")
+        return out
+    if doc_start.dtype != torch.int32 or doc_start.shape != (B, T) or doc_start.device != dev:
+        raise ValueError(f"doc_start must be int32 [B, T] = {(B, T)} on {dev}")
+    if doc_start.stride(1) != 1:
+        raise ValueError("doc_start: the last dimension must be contiguous")
+    if not torch.cuda.is_current_stream_capturing():
+        pos = offset + torch.arange(T, device=dev, dtype=torch.int32)
+        if bool(((doc_start < 0) | (doc_start > pos)).any()) or \
+                bool((doc_start[:, 1:] < doc_start[:, :-1]).any()):
+            raise ValueError("doc_start must be non-decreasing and in [0, the query's position]")
+    st = lib().forge_attn_prefill_docs(dtype_code(q), B, T, H, K, D, _ptr(q), q.stride(0), q.stride(1),
+                                       q.stride(2), _ptr(w), float(eps), flags, _ptr(c), _ptr(s), s_t,
+                                       _ptr(k), _ptr(v), k.stride(0), k.stride(1), k.stride(2),
+                                       int(offset), int(window), float(scale), _ptr(doc_start),
+                                       doc_start.stride(0), _ptr(out), out.stride(0), out.stride(1),
+                                       out.stride(2), _stream(dev))
+    check(st, "forge_attn_prefill_docs")
     return out
 
 

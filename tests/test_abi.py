@@ -32,7 +32,7 @@ def test_every_declared_symbol_is_exported_and_bound():
     assert {"forge_abi_version", "forge_last_error", "forge_head_norm_rope", "forge_kv_append",
             "forge_attn_decode", "forge_attn_decode_append", "forge_attn_decode_chunk",
             "forge_attn_decode_chunk_uniform", "forge_attn_decode_workspace_bytes",
-            "forge_attn_prefill"} <= names
+            "forge_attn_prefill", "forge_attn_prefill_docs"} <= names
     raw = C.CDLL(str(_lib.LIB_PATH))
     for n in names:
         assert hasattr(raw, n), n

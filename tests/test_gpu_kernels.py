@@ -343,6 +343,77 @@ def test_prefill_sliding_window(window):
     assert max_abs(got, ref) <= 2e-2
 
 
+def _doc_ids(lengths_per_row):
+    """[B, T] document numbers from each row's document lengths."""
+    rows = [torch.cat([torch.full((n,), d) for d, n in enumerate(ls)]) for ls in lengths_per_row]
+    return torch.stack(rows)
+
+
+def _doc_starts_of(doc_ids):
+    """First position of each position's document (documents are contiguous runs)."""
+    B, T = doc_ids.shape
+    start = torch.zeros(B, T, dtype=torch.int32)
+    for b in range(B):
+        for t in range(1, T):
+            start[b, t] = start[b, t - 1] if doc_ids[b, t] == doc_ids[b, t - 1] else t
+    return start
+
+
+# documents per row: a 1-token document, boundaries on and off the 64/128-key tiles, one
+# document longer than a query block, and a row that is one document
+DOC_LAYOUTS = [[[5, 1, 122, 64, 256, 252], [700]],
+               [[128, 128, 1, 63, 380], [64] * 10 + [60]]]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("window", [0, 100])
+def test_prefill_with_documents(dtype, D, layout, window):
+    """forge_attn_prefill_docs: causal and within each query's document (the reference's
+    same_doc mask, transformer.py:271-275 with attention.py:184-186), against the oracle's
+    SDPA with that mask (K/V heads repeated, as the reference does with a document mask)."""
+    g = gen(900 + D + layout + window)
+    docs = _doc_ids(DOC_LAYOUTS[layout])
+    B, T = docs.shape
+    H, K = 4, 2
+    q = randn(g, B, T, H, D, dtype=dtype).transpose(1, 2)
+    w = (1 + 0.1 * randn(g, D)).to(dtype)
+    kc = randn(g, B, K, T, D, dtype=dtype)
+    vc = randn(g, B, K, T, D, dtype=dtype)
+    c, s = tables(D, T, 1e4)
+    qn = oracle.head_norm_rope(q, w, 1e-6, c, s)
+    ref = oracle.sdpa(qn.float(), kc.float(), vc.float(), 0, window, scale_of(D),
+                      oracle.document_mask(docs)).transpose(1, 2)
+    ds = _doc_starts_of(docs).to(DEV)
+    got = ops().attn_prefill(q.to(DEV), kc.to(DEV), vc.to(DEV), scale=scale_of(D), window=window,
+                             q_weight=w.to(DEV), eps=1e-6, norm_q=True, cos=c.to(DEV), sin=s.to(DEV),
+                             doc_start=ds).cpu()
+    assert max_abs(got, ref) <= tol(dtype)
+
+
+def test_prefill_one_document_equals_plain_prefill():
+    """Document starts all 0 (one document per row) change nothing, bit for bit."""
+    g = gen(950)
+    B, H, K, D, T = 2, 8, 2, 128, 333
+    q = randn(g, B, H, T, D, dtype=torch.bfloat16).to(DEV)
+    kc = randn(g, B, K, T, D, dtype=torch.bfloat16).to(DEV)
+    vc = randn(g, B, K, T, D, dtype=torch.bfloat16).to(DEV)
+    a = ops().attn_prefill(q, kc, vc, scale=0.1)
+    b = ops().attn_prefill(q, kc, vc, scale=0.1, doc_start=torch.zeros(B, T, dtype=torch.int32, device=DEV))
+    assert torch.equal(a, b)
+
+
+def test_prefill_documents_rejects_bad_starts():
+    q = torch.zeros(1, 2, 40, 64, dtype=torch.bfloat16, device=DEV)
+    k = torch.zeros(1, 1, 40, 64, dtype=torch.bfloat16, device=DEV)
+    bad = [torch.arange(40, dtype=torch.int32).flip(0)[None],       # decreasing
+           torch.full((1, 40), 5, dtype=torch.int32)]                 # after the first queries
+    for ds in bad:
+        with pytest.raises(ValueError):
+            ops().attn_prefill(q, k, k, scale=0.1, doc_start=ds.to(DEV))
+
+
 def test_prefill_rejects_fp32():
     q = torch.zeros(1, 2, 4, 128, device=DEV)
     with pytest.raises(ValueError):

@@ -267,6 +267,39 @@ def test_taps_on_the_hip_path():
         assert not torch.allclose(base, ablated)
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_document_mask_on_the_hip_path(hd, monkeypatch):
+    """The reference's document mask (transformer.py:271-275, from doc_ids) over a scored
+    window runs forge_attn_prefill_docs when the documents are contiguous runs, and agrees
+    with the module's own torch path (the reference's SDPA with _mask & same_doc); a mask
+    whose document ids repeat after a gap stays on the torch path."""
+    import oracle
+
+    Attention, ModelConfig, _ = _modules()
+    cfg = ModelConfig(vocab_size=10, d_model=8 * hd, n_heads=8, n_kv_heads=2, head_size=hd,
+                      qk_norm=True, rope_theta=1e4, n_layers=1)
+    torch.manual_seed(3)
+    a = Attention(cfg, 0).eval().to(DEV, torch.bfloat16)
+    B, T = 2, 300
+    x = torch.randn(B, T, 8 * hd, device=DEV, dtype=torch.bfloat16)
+    cos, sin = (t.to(DEV) for t in oracle.rope_tables(hd, T, 1e4))
+    docs = torch.stack([torch.repeat_interleave(torch.arange(4), torch.tensor([70, 1, 129, 100])),
+                        torch.repeat_interleave(torch.arange(3), torch.tensor([64, 64, 172]))]).to(DEV)
+    same_doc = oracle.document_mask(docs)
+    with torch.no_grad():
+        got = a(x, cos, sin, same_doc=same_doc).float()
+        assert a.last_path == "hip-prefill-docs"
+        monkeypatch.setenv("SLEUTH_AMD_NO_HIP", "1")
+        want = a(x, cos, sin, same_doc=same_doc).float()
+        assert a.last_path == "torch"
+        monkeypatch.delenv("SLEUTH_AMD_NO_HIP")
+        assert (got - want).abs().max().item() <= 2e-2
+        gapped = docs.clone()
+        gapped[0, 250:] = 0                         # document 0 again, after documents 1-3
+        a(x, cos, sin, same_doc=oracle.document_mask(gapped))
+        assert a.last_path == "torch"
+
+
 @pytest.mark.parametrize("host_cache", [False, True])
 def test_static_step_equals_normal_step_on_gpu(host_cache):
     """A static (graph-ready) step of 5 tokens == the normal path (tests/test_cuda_graph.py:81-95),

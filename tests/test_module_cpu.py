@@ -305,7 +305,17 @@ def test_shared_layers_each_application_has_its_own_cache_slot():
 def test_hip_gate_on_cpu():
     cfg = ModelConfig(vocab_size=10, d_model=64, n_heads=4)
     a = Attention(cfg, 0)
-    assert not a._use_hip(torch.zeros(1, 4, 1, 16), None, None)
+    assert a._use_hip(torch.zeros(1, 4, 1, 16), None, None) == (False, None)
+
+
+def test_document_mask_on_cpu_takes_the_torch_path():
+    """A document mask on CPU tensors is the reference's eager path (the kernels' document
+    starts are taken from GPU masks only; their GPU test is in test_gpu_module.py)."""
+    import oracle
+    from sleuth_amd import attention as att
+
+    m = oracle.document_mask(torch.tensor([[0, 0, 1, 1, 1]]))
+    assert att._doc_starts(m, 1, 5) is None
 
 
 @pytest.mark.parametrize("sliding,n_past", [(False, 1), (False, 40), (True, 5), (True, 40)])

@@ -335,6 +335,34 @@ def _raises(check, fn):
         check(fn)
 
 
+def check_document_attention(fn) -> None:
+    """Document-masked attention fn(q, k, v, doc_ids, window, scale) -> [B,H,T,hd] against
+    the float64 loops restricted to each query's document, and against each document of a
+    packed row attended alone at the same positions (the reference's note on doc_ids,
+    transformer.py:258-264: a masked document behaves as if it were alone)."""
+    g = torch.Generator().manual_seed(21)
+    B, H, K, T, D = 2, 4, 2, 19, 8
+    q = torch.randn(B, H, T, D, generator=g, dtype=torch.float64)
+    k = torch.randn(B, K, T, D, generator=g, dtype=torch.float64)
+    v = torch.randn(B, K, T, D, generator=g, dtype=torch.float64)
+    docs = torch.tensor([[0] * 5 + [1] * 1 + [2] * 9 + [3] * 4, [7] * 11 + [8] * 8])
+    for window in (0, 4):
+        got = fn(q, k, v, docs, window, 0.35)
+        want = ref.brute_attention(q, k, v, 0, window, 0.35, doc_ids=docs)
+        torch.testing.assert_close(got.double(), want, atol=1e-10, rtol=0)
+    got = fn(q, k, v, docs, 0, 0.35)
+    for b in range(B):
+        for d in docs[b].unique():
+            idx = (docs[b] == d).nonzero().view(-1)
+            a, z = int(idx[0]), int(idx[-1]) + 1
+            alone = ref.sdpa(q[b:b + 1, :, a:z], k[b:b + 1, :, a:z], v[b:b + 1, :, a:z], 0, 0, 0.35)
+            torch.testing.assert_close(got[b:b + 1, :, a:z].double(), alone, atol=1e-10, rtol=0)
+
+
+def test_document_attention_pinned():
+    check_document_attention(lambda q, k, v, d, w, sc: ref.sdpa(q, k, v, 0, w, sc, ref.document_mask(d)))
+
+
 def test_pins_catch_planted_mistakes():
     # RoPE: inverse frequencies over arange(0, d) instead of arange(0, d, 2)
     def bad_tables(d, L, theta):
@@ -366,6 +394,13 @@ def test_pins_catch_planted_mistakes():
     # attention: scale applied twice / window ignored
     _raises(check_attention, lambda q, k, v, off, win, sc: ref.sdpa(q, k, v, off, win, sc * sc))
     _raises(check_attention, lambda q, k, v, off, win, sc: ref.sdpa(q, k, v, off, 0, sc))
+    # documents: the mask shifted by one position, or the causal part dropped
+    _raises(check_document_attention,
+            lambda q, k, v, d, w, sc: ref.sdpa(q, k, v, 0, w, sc, ref.document_mask(torch.roll(d, 1, 1))))
+    _raises(check_document_attention,
+            lambda q, k, v, d, w, sc: F.scaled_dot_product_attention(
+                q, k.repeat_interleave(2, 1), v.repeat_interleave(2, 1), scale=sc,
+                attn_mask=ref.document_mask(d) & (ref.attention_mask(q.shape[2], q.shape[2], 0, w) | True)))
     # drafter: the query's own position counted as stored / the window one key wider
     _raises(check_drafter, lambda q, k, v, n, win, sc: ref.drafter_attention(q, k, v, min(n + 1, k.shape[2]), win, sc))
     _raises(check_drafter, lambda q, k, v, n, win, sc: ref.drafter_attention(q, k, v, n, win + 1 if win else 0, sc))
