@@ -306,7 +306,7 @@ class Attention(nn.Module):
             ops.kv_append(k, v, kc, vc, norm_v=norm_v, **pos_kw, **k_args)
             self.last_path = "hip-prefill" if docs is None else "hip-prefill-docs"
             return ops.attn_prefill(q, kc, vc, scale=self.scale, offset=offset, window=self.window,
-                                    doc_start=docs, **q_args)
+                                    doc_start=docs, check_doc_start=False, **q_args)
         if docs is not None:
             raise RuntimeError("a document mask needs the prefill path (no cache, T > 16)")
         # the cache write and the attention in one call (one launch where the shape allows);

@@ -354,14 +354,15 @@ def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: fl
                  window: int = 0, q_weight: torch.Tensor | None = None, eps: float = 1e-6,
                  norm_q: bool = False, cos: torch.Tensor | None = None,
                  sin: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                 doc_start: torch.Tensor | None = None) -> torch.Tensor:
+                 doc_start: torch.Tensor | None = None, check_doc_start: bool = True) -> torch.Tensor:
     """Causal flash attention on MFMA: queries at positions offset..offset+T-1 over keys
     0..offset+T-1 of k/v [B,K,>=offset+T,D]. Returns [B,T,H,D].
 
     doc_start: [B, T] int32, the position of the first token of each query's document (the
     reference's document mask, transformer.py:271-275): query t also sees no key before it.
-    It must be non-decreasing along T and at most the query's own position (checked, except
-    under graph capture)."""
+    It must be non-decreasing along T and at most the query's own position: checked here
+    (two host synchronisations) unless check_doc_start is False, for a caller that built
+    it so (the module's own starts, taken from the mask), or under graph capture."""
     B, H, T, D = q.shape
     Bk, K, S, Dk = k.shape
     if Bk != B or Dk != D or v.shape != k.shape or H % K:
@@ -396,7 +397,7 @@ def attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: fl
         raise ValueError(f"doc_start must be int32 [B, T] = {(B, T)} on {dev}")
     if doc_start.stride(1) != 1:
         raise ValueError("doc_start: the last dimension must be contiguous")
-    if not torch.cuda.is_current_stream_capturing():
+    if check_doc_start and not torch.cuda.is_current_stream_capturing():
         pos = offset + torch.arange(T, device=dev, dtype=torch.int32)
         if bool(((doc_start < 0) | (doc_start > pos)).any()) or \
                 bool((doc_start[:, 1:] < doc_start[:, :-1]).any()):
