@@ -923,27 +923,28 @@ template <int N> __device__ __forceinline__ void vwait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// One unit of the MFMA verify path: rows rb*32 .. of KV head kvh of batch row b (whose first
+// new token sits at position `base`), keys of chunk c_in (absolute; with p.span_chunks,
+// counted from the unit's first visible chunk). The caller passes block-uniform arguments
+// and a converged block; the unit may leave early, block-uniformly, and uses all of the
+// dynamic LDS `smem`.
 template <typename T, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-void verify_mfma_kernel(SplitParams p) {
+__device__ __forceinline__ void verify_unit(const SplitParams& p, char* smem, const int b,
+                                            const int base, const int kvh, const int rb,
+                                            const int c_in) {
   using V8 = typename VMfma<T>::vec;
   using TL = VerifyTile<D>;
   constexpr int BN = TL::BN;
   constexpr int KSTEPS = D / 16;
   constexpr int DBW = TL::DW / 32;  // 32-channel blocks per wave
-  extern __shared__ __attribute__((aligned(1024))) char smem[];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
   const int n = lane & 31;
   const int hi = lane >> 5;
-  const int kvh = blockIdx.y % p.K;
-  const int rb = blockIdx.y / p.K;
-  const int b = blockIdx.z;
 
   // this lane's row and its visible keys; the unit's key span (union over valid rows)
-  const int base = (int)row_base(p.row_pos, p.pos_dev, p.pos0, b);
   const int flat = rb * TL::ROWS + n;
   const bool valid = flat < p.rows_total;
   const int t = valid ? flat / p.G : 0;
@@ -958,7 +959,7 @@ void verify_mfma_kernel(SplitParams p) {
     visible_range32(base + rb * TL::ROWS / p.G, p.window, (int)p.max_len, umin, dummy);
     visible_range32(base + r_hi / p.G, p.window, (int)p.max_len, dummy, umax);
   }
-  const int c = p.span_chunks ? umin / p.chunk + (int)blockIdx.x : (int)blockIdx.x;  // absolute chunk
+  const int c = p.span_chunks ? umin / p.chunk + c_in : c_in;  // absolute chunk
   const int c0 = c * p.chunk;
   if (c >= p.max_chunks || c0 > umax || c0 + p.chunk - 1 < umin) return;  // block-uniform
 
@@ -1335,6 +1336,94 @@ void verify_mfma_kernel(SplitParams p) {
   }
 }
 
+// Rows of a persistent MFMA verify launch held in LDS (their first new position and the
+// prefix sums of their units): 4 KB, within the 80 KB a block may use for two blocks per CU
+// at head dim 128.
+constexpr int kVerifyPersistRows = 512;
+
+// MFMA verify kernel, dense grid: one block per (chunk, KV head x row block, batch row).
+template <typename T, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void verify_mfma_kernel(SplitParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const int b = blockIdx.z;
+  verify_unit<T, D>(p, smem, b, (int)row_base(p.row_pos, p.pos_dev, p.pos0, b), blockIdx.y % p.K,
+                    blockIdx.y / p.K, blockIdx.x);
+}
+
+// MFMA verify kernel, persistent (positions in device memory): verify_blocks_per_cu blocks
+// per CU take the units (row, KV head x row block, chunk) of every row's own chunk range by
+// ticket, as splitk_kernel does, so a ragged batch spends no blocks on chunks past a row's
+// end and the blocks that stream faster take more units. (A kernel of its own: with both
+// grids in one, the dense grid's registers grew from 150 to 212 at head dim 128.)
+template <typename T, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void verify_mfma_persistent_kernel(SplitParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  __shared__ int sh_pref[kVerifyPersistRows + 1];
+  __shared__ int sh_base[kVerifyPersistRows];
+  __shared__ int sh_ticket[2];
+  const int tid = threadIdx.x;
+  constexpr int ROWS = VerifyTile<D>::ROWS;
+  const int per_row = p.K * ((p.rows_total + ROWS - 1) / ROWS);
+  // chunks of each row: the union of its T queries' visible keys (wave 0 scans the rows)
+  auto row_chunks = [&](int base) {
+    int lo, hi0, lo1, hi;
+    visible_range32(base, p.window, (int)p.max_len, lo, hi0);
+    visible_range32(base + p.T - 1, p.window, (int)p.max_len, lo1, hi);
+    const int cmin = lo / p.chunk;
+    int cmax = hi / p.chunk;
+    if (cmax > p.max_chunks - 1) cmax = p.max_chunks - 1;
+    return (hi >= lo && cmax >= cmin) ? cmax - cmin + 1 : 0;
+  };
+  for (int b = tid; b < p.B; b += blockDim.x) sh_base[b] = (int)row_base(p.row_pos, p.pos_dev, p.pos0, b);
+  __syncthreads();
+  if (tid < kWave) {
+    const int seg = (p.B + kWave - 1) / kWave;
+    const int r0 = tid * seg;
+    const int r1 = r0 + seg < p.B ? r0 + seg : p.B;
+    int sum = 0;
+    for (int r = r0; r < r1; ++r) sum += row_chunks(sh_base[r]) * per_row;
+    int incl = sum;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int v = __shfl_up(incl, d, kWave);
+      if (tid >= d) incl += v;
+    }
+    int run = incl - sum;
+    for (int r = r0; r < r1; ++r) {
+      sh_pref[r] = run;
+      run += row_chunks(sh_base[r]) * per_row;
+    }
+    if (tid == kWave - 1) sh_pref[p.B] = incl;
+  }
+  __syncthreads();
+  const int total = sh_pref[p.B];
+  // Block i starts with unit i, then takes units by ticket; the ticket slots alternate, as
+  // in splitk_kernel (a unit may leave without a block barrier).
+  int parity = 0;
+  for (int u = blockIdx.x; u < total; u = __builtin_amdgcn_readfirstlane(sh_ticket[parity]), parity ^= 1) {
+    int next = 0;
+    if (tid == 0) next = atomicAdd(p.ws_ctr, 1);  // read after the unit: its round trip hides
+    int lo = 0, hi = p.B - 1;  // last row with sh_pref[row] <= u
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (__builtin_amdgcn_readfirstlane(sh_pref[mid]) <= u) lo = mid;
+      else hi = mid - 1;
+    }
+    const int base = __builtin_amdgcn_readfirstlane(sh_base[lo]);
+    const int o = u - __builtin_amdgcn_readfirstlane(sh_pref[lo]);
+    const int nch = row_chunks(base);
+    const int pr = o / nch;
+    int kmin, kmax;
+    visible_range32(base, p.window, (int)p.max_len, kmin, kmax);  // the row's first chunk
+    // a row's chunks last to first (the last one's unit also makes the new keys)
+    verify_unit<T, D>(p, smem, lo, base, pr % p.K, pr / p.K, kmin / p.chunk + (nch - 1 - o % nch));
+    if (tid == 0) sh_ticket[parity] = (int)gridDim.x + next;
+    __syncthreads();  // the next unit reuses the LDS stages and tables; the ticket is visible
+  }
+}
+
 // ---------------------------------------------------------------- host side
 static int vec_of(int dtype) { return dtype == FORGE_F32 ? 4 : 8; }
 
@@ -1572,15 +1661,37 @@ static int launch_verify_d(SplitParams p, hipStream_t s) {
   static bool attr_set = false;  // raise the dynamic LDS limit once per kernel
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_mfma_kernel<T, D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, TL::LDS_BYTES) != hipSuccess ||
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_mfma_persistent_kernel<T, D>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, TL::LDS_BYTES) != hipSuccess)
       return set_error("forge_attn_decode: cannot reserve the LDS the kernel needs");
     attr_set = true;
   }
   const int n_rb = (p.rows_total + kVerifyRows - 1) / kVerifyRows;
-  if ((int64_t)p.K * n_rb > 65535 || p.B > 65535) return set_error("grid too large");
-  p.persist = 0;
-  const dim3 grid((unsigned)dense_chunks(p), (unsigned)(p.K * n_rb), (unsigned)p.B);
-  hipLaunchKernelGGL((verify_mfma_kernel<T, D>), grid, dim3(256), TL::LDS_BYTES, s, p);
+  dim3 grid;
+  // persistent where the lengths live on the device, as for the split kernel
+  const bool device_lengths = p.row_pos != nullptr || p.pos_dev != nullptr;
+  if (device_lengths && p.B <= kVerifyPersistRows && p.ws_ctr) {
+    const int64_t upper = (int64_t)p.B * p.K * n_rb * p.max_chunks;
+    if (upper >= (1LL << 31)) return set_error("forge_attn_decode: too many work units");
+    int64_t blocks = (int64_t)verify_blocks_per_cu(D) * device_cus();
+    if (upper < blocks) blocks = upper;
+    p.persist = 1;
+    grid = dim3((unsigned)blocks);
+    if (!p.ws_zeroed) {
+      hipLaunchKernelGGL(ticket_reset_kernel, dim3(1), dim3(64), 0, s, p.ws_ctr);
+      const int st0 = check_launch();
+      if (st0) return st0;
+    }
+  } else {
+    if ((int64_t)p.K * n_rb > 65535 || p.B > 65535) return set_error("grid too large");
+    p.persist = 0;
+    grid = dim3((unsigned)dense_chunks(p), (unsigned)(p.K * n_rb), (unsigned)p.B);
+  }
+  if (p.persist)
+    hipLaunchKernelGGL((verify_mfma_persistent_kernel<T, D>), grid, dim3(256), TL::LDS_BYTES, s, p);
+  else
+    hipLaunchKernelGGL((verify_mfma_kernel<T, D>), grid, dim3(256), TL::LDS_BYTES, s, p);
   int st = check_launch();
   if (st || p.max_chunks < 2) return st;
   const int64_t nrows = (int64_t)p.B * p.H * p.T;

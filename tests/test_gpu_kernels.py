@@ -245,13 +245,16 @@ def test_persistent_verify_row_blocks_with_early_returns(dtype):
         assert torch.equal(dense, persistent)
 
 
-@pytest.mark.parametrize("T,H,K", [(1, 16, 8), (2, 8, 8)])
+@pytest.mark.parametrize("T,H,K", [(1, 16, 8), (2, 8, 8), (1, 32, 8), (5, 32, 8), (4, 8, 1)])
 def test_persistent_runs_equal_per_row_dense_calls(T, H, K):
     """Ragged rows on the persistent grid (64 rows, up to 47 chunks each, units taken by
     ticket in any order) equal bit for bit the same rows computed one at a time on the dense
-    grid (T = 2: two query rows with different last keys in one row block)."""
+    grid (T = 2: two query rows with different last keys in one row block). G >= 4 runs the
+    MFMA verify kernel, persistent too (at T = 1 and 5 for 32 q / 8 KV heads, and the MQA
+    verify shape at head dim 256)."""
     g = gen(61)
-    B, D, chunk = 64, 128, 128
+    B, chunk = 64, 128
+    D = 256 if K == 1 else 128
     lens = torch.randint(T, 6000, (B,), generator=torch.Generator().manual_seed(61)).tolist()
     L = max(lens)
     kc = randn(g, B, K, L, D, dtype=torch.bfloat16).to(DEV)
