@@ -167,8 +167,8 @@ int forge_attn_decode_noalloc(int dtype, int B, int T, int H, int K, int D, cons
  * for the signature but does not enter, so decode and verify steps of one layer agree. */
 int forge_attn_decode_chunk(int dtype, int B, int T, int H, int K, int D, int64_t max_kv_len);
 
-/* Keys per split for calls whose rows all start at one host position (pos0, no row_pos or
- * pos_dev): every row has the same length, so the split only has to spread the work over
+/* Keys per split for calls whose rows all start at one position (pos0 or pos_dev, no
+ * row_pos): every row has the same length, so the split only has to spread the work over
  * the CUs, and rows are not split at all when the (row, KV head) pairs already fill them.
  * Use it for such calls in place of forge_attn_decode_chunk (no counterpart in the
  * reference: a tuning query, like forge_attn_decode_chunk). T does not enter. */

@@ -299,7 +299,7 @@ class Attention(nn.Module):
             # from the cache's capacity and T = 1: every step of this layer, decode or verify,
             # splits its rows at the same keys
             chunk = ops.decode_chunk(q.dtype, B, 1, H, self.n_kv, hd, cache.max_len, self.window,
-                                     uniform="pos" in pos_kw)
+                                     uniform="row_pos" not in pos_kw)
 
         if T > DECODE_MAX_T and offset is not None and ops.prefill_supported(q) and \
                 (q_args["cos"] is None or q_args["cos"].dim() == 2):

@@ -1351,8 +1351,8 @@ void verify_mfma_kernel(SplitParams p) {
                     blockIdx.y / p.K, blockIdx.x);
 }
 
-// MFMA verify kernel, persistent (positions in device memory): verify_blocks_per_cu blocks
-// per CU take the units (row, KV head x row block, chunk) of every row's own chunk range by
+// MFMA verify kernel, persistent (per-row positions in device memory): verify_blocks_per_cu
+// blocks per CU take the units (row, KV head x row block, chunk) of every row's own chunk range by
 // ticket, as splitk_kernel does, so a ragged batch spends no blocks on chunks past a row's
 // end and the blocks that stream faster take more units. (A kernel of its own: with both
 // grids in one, the dense grid's registers grew from 150 to 212 at head dim 128.)
@@ -1617,12 +1617,13 @@ static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
     default: return set_error("internal: rows per block");
   }
   dim3 grid;
-  // Persistent only where the lengths live on the device (ragged rows, graph steps): there
-  // it saves the blocks a dense grid would spend past each row's end. With one host-known
-  // position the dense grid has no such blocks, and the hardware's dynamic block dispatch
-  // balances uneven per-CU bandwidth better than a fixed assignment does.
-  const bool device_lengths = p.row_pos != nullptr || p.pos_dev != nullptr;
-  if (device_lengths && p.B <= kPersistMaxRows && p.ws_ctr) {
+  // Persistent only for per-row lengths (ragged rows): there it saves the blocks a dense
+  // grid would spend past each row's end. With one position for every row, host-known or on
+  // the device (graph steps), the dense grid is faster (C3 decode with the position on the
+  // device: 163.7 us against 186.5 us persistent; 169.8 against 186.4 us in a cache of 4x
+  // the rows' length), and the hardware's dynamic block dispatch balances uneven per-CU
+  // bandwidth better than a fixed assignment does.
+  if (p.row_pos != nullptr && p.B <= kPersistMaxRows && p.ws_ctr) {
     const int64_t upper = (int64_t)p.B * p.K * n_rb * p.max_chunks;
     int blocks = resident_blocks(kern);
     if (blocks <= 0) return set_error("forge_attn_decode: cannot query the device");
@@ -1669,9 +1670,10 @@ static int launch_verify_d(SplitParams p, hipStream_t s) {
   }
   const int n_rb = (p.rows_total + kVerifyRows - 1) / kVerifyRows;
   dim3 grid;
-  // persistent where the lengths live on the device, as for the split kernel
-  const bool device_lengths = p.row_pos != nullptr || p.pos_dev != nullptr;
-  if (device_lengths && p.B <= kVerifyPersistRows && p.ws_ctr) {
+  // Persistent for per-row lengths. One device-held position for every row (a graph step)
+  // keeps the dense grid: its rows end together, and the persistent launch's ticket reset
+  // and set-up cost C5 (8 rows) 35.2 against 29.1 us per graph-replayed call.
+  if (p.row_pos != nullptr && p.B <= kVerifyPersistRows && p.ws_ctr) {
     const int64_t upper = (int64_t)p.B * p.K * n_rb * p.max_chunks;
     if (upper >= (1LL << 31)) return set_error("forge_attn_decode: too many work units");
     int64_t blocks = (int64_t)verify_blocks_per_cu(D) * device_cus();

@@ -161,8 +161,9 @@ def decode_chunk(dtype: torch.dtype, B: int, T: int, H: int, K: int, D: int, max
     """Default split-K chunk. T does not enter (decode and verify of a model share chunk
     boundaries, so verify rows equal single-token decodes bit for bit); with a sliding window
     it is sized for the keys a row can see, window + 16, not the cache length. `uniform`:
-    every row of the calls starts at one host position (`pos`), so rows have one length and
-    the chunk only spreads the work over the CUs (forge_attn_decode_chunk_uniform)."""
+    every row of the calls starts at one position (`pos`, or `pos_dev` on the device), so
+    rows have one length and the chunk only spreads the work over the CUs
+    (forge_attn_decode_chunk_uniform)."""
     span = int(max_kv_len)
     if window > 0 and window + DECODE_CHUNK_MAX_T < span:
         span = window + DECODE_CHUNK_MAX_T
@@ -202,7 +203,7 @@ def _decode_args(q, k_cache, v_cache, scale, pos, pos_dev, row_pos, max_kv_len, 
     elif out.shape != (B, T, H, D) or out.dtype != q.dtype:
         raise ValueError(f"out must be [B,T,H,D] = {(B, T, H, D)} {q.dtype}")
     if chunk <= 0:  # from the cache's capacity, not this call's length: stable across steps
-        chunk = decode_chunk(q.dtype, B, T, H, K, D, max_len, window, uniform=rp is None and pd is None)
+        chunk = decode_chunk(q.dtype, B, T, H, K, D, max_len, window, uniform=rp is None)
     args = (dtype_code(q), B, T, H, K, D, _ptr(q), q.stride(0), q.stride(1), q.stride(2),
             _ptr(w), float(eps), flags, _ptr(c), _ptr(s), s_b, s_t,
             _ptr(k_cache), _ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
