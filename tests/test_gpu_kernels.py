@@ -184,8 +184,8 @@ def test_verify_rows_equal_single_decodes_bitwise(dtype, H, K, D):
 
 @pytest.mark.parametrize("H,K", [(16, 8), (8, 1)])
 def test_decode_pos_dev_matches_host_pos(H, K):
-    """Device-held position (persistent grid) equals the host position (dense grid) bit for
-    bit, on the VALU kernel (G = 2) and the wide-group MFMA kernel (G = 8)."""
+    """Device-held position equals the host position bit for bit at one chunk, on the VALU
+    kernel (G = 2) and the wide-group MFMA kernel (G = 8)."""
     g = gen(9)
     B, D, T, L = 2, 128, 3, 900
     kc = randn(g, B, K, 1024, D, dtype=torch.bfloat16).to(DEV)
@@ -195,6 +195,31 @@ def test_decode_pos_dev_matches_host_pos(H, K):
     b = ops().attn_decode(q, kc, vc, scale=0.1, pos_dev=torch.tensor([L - T], device=DEV),
                           max_kv_len=1024, chunk=128)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("cap", [2048, 8192])
+def test_decode_pos_dev_default_chunk(cap):
+    """One device-held position for every row (graph decode steps) takes the host position's
+    default chunk (the uniform rule) and dense grid: 32 rows x 8 KV heads fill the CUs, so
+    rows of 2,000 keys stay unsplit in a cache of their length and of four times it, where
+    the per-row rule would split them. Bit for bit the host-position call, within bf16
+    tolerance of the oracle, and blind to the 1e4-poisoned cache past the rows' end."""
+    g = gen(41)
+    B, H, K, D, L = 32, 16, 8, 128, 2000
+    kc = randn(g, B, K, cap, D, dtype=torch.bfloat16)
+    vc = randn(g, B, K, cap, D, dtype=torch.bfloat16)
+    kc[:, :, L:] = 1e4
+    vc[:, :, L:] = 1e4
+    q = randn(g, B, H, 1, D, dtype=torch.bfloat16)
+    assert ops().decode_chunk(torch.bfloat16, B, 1, H, K, D, cap, uniform=True) != \
+        ops().decode_chunk(torch.bfloat16, B, 1, H, K, D, cap)
+    kd, vd, qd = kc.to(DEV), vc.to(DEV), q.to(DEV)
+    a = ops().attn_decode(qd, kd, vd, scale=scale_of(D), pos=L - 1)
+    b = ops().attn_decode(qd, kd, vd, scale=scale_of(D), max_kv_len=cap,
+                          pos_dev=torch.tensor([L - 1], dtype=torch.int64, device=DEV))
+    assert torch.equal(a, b)
+    ref = oracle.ragged_decode(q.float(), kc[:, :, :L].float(), vc[:, :, :L].float(), [L] * B, 0, scale_of(D))
+    assert max_abs(b.cpu(), ref.transpose(1, 2)) <= 2e-2
 
 
 @pytest.mark.parametrize("B", [8, 300])
