@@ -1491,19 +1491,27 @@ static int verify_round_chunk(int B, int H, int K, int D, int64_t max_kv_len) {
   return (int)(chunk < min_chunk ? min_chunk : chunk);
 }
 
-// Longest chunk of the MFMA verify path for device-held or per-row positions: a ragged
-// batch's long rows would otherwise be few long units that finish last (C4 lengths at
-// 32 q / 8 KV heads: 1012 us per decode step at 512-key chunks against 1205 us for one chunk
-// per row; 28 q / 4 KV heads, 32 rows: 208 against 304 us; 8 q / 1 KV head, T = 4, 32 rows:
-// 72 against 90 us; 256-key chunks were as fast or slower, 1024 slower for all three).
+// Longest chunk of the MFMA verify path on the dense grid (per-row positions beyond the
+// persistent grid's rows, and the host-position rule's cap): a ragged batch's long rows
+// would otherwise be few long units that finish last (C4 lengths at 32 q / 8 KV heads:
+// 1012 us per decode step at 512-key chunks against 1205 us for one chunk per row; 28 q /
+// 4 KV heads, 32 rows: 208 against 304 us; 8 q / 1 KV head, T = 4, 32 rows: 72 against
+// 90 us; 256-key chunks were as fast or slower, 1024 slower for all three).
 constexpr int kMaxVerifyChunk = 512;
+// The same on the persistent grid (per-row positions, up to kVerifyPersistRows rows), whose
+// tickets leave no block idle behind a long row: there fewer, longer units win (C4 lengths
+// at 32 q / 8 KV heads: 688.5 us per decode step at 1024-key chunks against 723.6 at 512
+// and 712.1 at 2048; T = 5 verify 794.3 against 853.1; 28 q / 4 KV heads, 32 rows: 186.0
+// against 192.6; 8 q / 1 KV head, T = 4: 58.7 against 66.2 us, and 77.0 at 2048).
+constexpr int kMaxVerifyChunkPersist = 1024;
 
 static int auto_chunk(int dtype, int B, int /*T*/, int H, int K, int D, int64_t max_kv_len) {
   const int T = 1;
   const int G = H / K;
   if (use_verify_mfma(dtype, D, G)) {
     const int chunk = verify_round_chunk(B, H, K, D, max_kv_len);
-    return chunk < kMaxVerifyChunk ? chunk : kMaxVerifyChunk;
+    const int cap = B <= kVerifyPersistRows ? kMaxVerifyChunkPersist : kMaxVerifyChunk;
+    return chunk < cap ? chunk : cap;
   }
   const int rows = rows_per_block(G * T);
   const int64_t n_rb = (G * T + rows - 1) / rows;

@@ -49,6 +49,10 @@ def test_host_only_functions():
     assert ws >= 64 * 16 * chunks * (128 * 4 + 8)
     assert lib.forge_attn_decode_workspace_bytes(_lib.BF16, 1, 1, 8, 4, 64, 50, 64) == 0  # one chunk
     assert lib.forge_attn_decode_chunk(_lib.BF16, 1, 1, 8, 3, 64, 100) == 0              # H % K != 0
+    # the MFMA path (G >= 4) for per-row positions: 1024-key chunks on the persistent grid
+    # (up to 512 rows), 512 on the dense grid beyond it
+    assert lib.forge_attn_decode_chunk(_lib.BF16, 64, 1, 32, 8, 128, 32768) == 1024
+    assert lib.forge_attn_decode_chunk(_lib.BF16, 600, 1, 32, 8, 128, 32768) == 512
 
 
 def test_uniform_chunk_rule():
