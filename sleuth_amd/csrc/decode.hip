@@ -44,8 +44,11 @@ constexpr int kMaxChunk = 1024;
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale: weights stay <= 2^8
 // Register buffers of the K/V pipeline (loads run PF - 1 iterations ahead): deeper where
 // few query rows leave the registers for it. Measured on C4-shaped ragged decode: PF 4
-// at 3 waves per SIMD streams faster than PF 3 at 4.
-template <int ROWS> constexpr int split_pf() { return ROWS <= 2 ? 4 : 3; }
+// at 3 waves per SIMD streams faster than PF 3 at 4; at 3-4 rows per block PF 4 at 2 waves
+// per SIMD (190 VGPRs) beats PF 3 at 3 (C4 lengths, 12 q / 4 KV heads: 339 against 355 us
+// per step; 16 q / 8 KV heads at T = 2: 669 against 685 us; 8 q / 8 KV heads at T = 4: 668
+// against 689 us; C2 19.6 against 19.8 us per graph-replayed call).
+template <int ROWS> constexpr int split_pf() { return ROWS <= 4 ? 4 : 3; }
 // New positions one lane group may hold in a call of forge_attn_decode_append (T up to
 // kNewPerLane times the key groups of the block; the host checks it).
 constexpr int kNewPerLane = 2;
@@ -568,6 +571,17 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
       compute_iter(it + j, kbuf[j], vbuf[j]);
+      // From 3 rows on, the accumulators are pinned final here, so this iteration's V
+      // registers are dead before their refill: left alone, the compiler sinks the V
+      // accumulation below the refill, keeps the refilled V rows in other registers and
+      // copies them back at the latch, which waits for all but the newest iteration's loads
+      // once per round (at 1-2 rows the same pin measured within noise, so it is left out).
+      if constexpr (ROWS > 2) {
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) asm volatile("" : "+v"(o[r][e]));
+      }
       // The refill stays below the compute, so the buffer keeps its registers across the
       // loop (no copies at the latch, which would wait for every load in flight).
       __builtin_amdgcn_sched_barrier(0);
@@ -659,8 +673,9 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
 constexpr int kPersistMaxRows = 2048;
 
 // Occupancy target: more waves hide more HBM latency, fewer leave registers for the
-// accumulators of ROWS query rows.
-template <int ROWS> constexpr int split_waves_per_eu() { return ROWS <= 4 ? 3 : 2; }
+// accumulators of ROWS query rows and the pipeline's buffers (the persistent grid holds two
+// blocks per CU, two waves per SIMD, whatever the target).
+template <int ROWS> constexpr int split_waves_per_eu() { return ROWS <= 2 ? 3 : 2; }
 
 template <typename T, int D, int ROWS>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(split_waves_per_eu<ROWS>())))
