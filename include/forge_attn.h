@@ -163,8 +163,10 @@ int forge_attn_decode_noalloc(int dtype, int B, int T, int H, int K, int D, cons
                               int chunk, void* out, int64_t sob, int64_t sot, int64_t soh,
                               void* stream);
 
-/* Keys per split for a row span of max_kv_len keys (pure host function). T is accepted
- * for the signature but does not enter, so decode and verify steps of one layer agree. */
+/* Keys per split for a row span of max_kv_len keys (pure host function): the rule for
+ * per-row positions (row_pos), whose ragged rows need chunks short enough to balance; at
+ * most 1024 keys (the MFMA path on more than 512 rows: 512). T is accepted for the
+ * signature but does not enter, so decode and verify steps of one layer agree. */
 int forge_attn_decode_chunk(int dtype, int B, int T, int H, int K, int D, int64_t max_kv_len);
 
 /* Keys per split for calls whose rows all start at one position (pos0 or pos_dev, no
