@@ -3,6 +3,8 @@ oracle on identical seeded inputs. Tolerances: fp32 max-abs <= 1e-4, bf16/fp16 <
 
 from __future__ import annotations
 
+import random
+
 import pytest
 import torch
 
@@ -235,6 +237,57 @@ def test_persistent_grid_equals_dense_grid_bitwise(B):
     rp = torch.full((B,), L - T, dtype=torch.int32, device=DEV)
     b = ops().attn_decode(q, kc, vc, scale=0.1, row_pos=rp, max_kv_len=768, chunk=128)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("case", range(200))
+def test_random_shapes_against_oracle(case):
+    """Seeded random shapes over every decode/verify kernel: dtype, head dim, head group
+    (G 1-8: the VALU kernel's 1-8-row blocks and the MFMA kernel from G = 4 at hd 128/256),
+    T up to 8, ragged per-row lengths (the persistent grids), windows and chunks (the
+    default rule, 256 and 1024 keys), against the oracle at the north-star tolerances."""
+    rng = random.Random(7000 + case)
+    dtype = rng.choice(DTYPES)
+    D = rng.choice([32, 64, 128, 256])
+    G, K = rng.choice([1, 2, 3, 4, 8]), rng.choice([1, 2, 4])
+    T = rng.choice([1, 1, 2, 3, 4, 5, 8])
+    lens = [rng.randint(T, 1200) for _ in range(rng.randint(1, 5))]
+    window = rng.choice([0, 0, 1, 9, 100])
+    chunk = rng.choice([0, 0, 256, 1024])
+    print(f"case {case}: {dtype} D={D} H={G * K} K={K} T={T} lens={lens} window={window} chunk={chunk}",
+          flush=True)
+    got, ref = _decode_case(9000 + case, dtype, len(lens), G * K, K, D, T, lens, window, chunk=chunk)
+    assert max_abs(got, ref) <= tol(dtype)
+
+
+@pytest.mark.parametrize("case", range(64))
+def test_random_position_modes_bitwise(case):
+    """Seeded random shapes with one length for every row, given three ways at one chunk:
+    the host position (dense grid), the device-held position (dense grid) and per-row
+    positions (the persistent grids): bit for bit the same outputs."""
+    rng = random.Random(8000 + case)
+    dtype = rng.choice(DTYPES)
+    D = rng.choice([64, 128, 256])
+    G, K = rng.choice([1, 2, 3, 4, 8]), rng.choice([1, 2, 4])
+    T = rng.choice([1, 2, 4, 5])
+    B = rng.randint(1, 6)
+    L = rng.randint(T, 2000)
+    cap = L + rng.randint(0, 300)
+    window = rng.choice([0, 0, 50])
+    chunk = rng.choice([256, 1024])
+    print(f"case {case}: {dtype} D={D} H={G * K} K={K} T={T} B={B} L={L} cap={cap} window={window} "
+          f"chunk={chunk}", flush=True)
+    g = gen(8100 + case)
+    kc = randn(g, B, K, cap, D, dtype=dtype).to(DEV)
+    vc = randn(g, B, K, cap, D, dtype=dtype).to(DEV)
+    q = randn(g, B, G * K, T, D, dtype=dtype).to(DEV)
+    kw = dict(scale=scale_of(D), window=window, chunk=chunk)
+    a = ops().attn_decode(q, kc, vc, pos=L - T, **kw)
+    b = ops().attn_decode(q, kc, vc, pos_dev=torch.tensor([L - T], dtype=torch.int64, device=DEV),
+                          max_kv_len=cap, **kw)
+    c = ops().attn_decode(q, kc, vc, row_pos=torch.full((B,), L - T, dtype=torch.int32, device=DEV),
+                          max_kv_len=cap, **kw)
+    assert torch.equal(a, b)
+    assert torch.equal(a, c)
 
 
 @pytest.mark.parametrize("B", [40, 300])
