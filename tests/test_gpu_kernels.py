@@ -418,6 +418,22 @@ def test_prefill(dtype, D, T, offset):
     assert max_abs(got, ref) <= tol(dtype)
 
 
+@pytest.mark.parametrize("case", range(48))
+def test_random_prefill_shapes_against_oracle(case):
+    """Seeded random prefill shapes: bf16/fp16, head dims 64/128/256, head groups 1-8,
+    T 17-700 (partial query and key tiles), offsets into a filled cache, windows."""
+    rng = random.Random(6000 + case)
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    D = rng.choice([64, 128, 256])
+    G, K = rng.choice([1, 2, 3, 4, 8]), rng.choice([1, 2])
+    B, T = rng.randint(1, 3), rng.randint(17, 700)
+    offset = rng.choice([0, 0, rng.randint(1, 600)])
+    window = rng.choice([0, 0, 1, 33, 256])
+    print(f"case {case}: {dtype} D={D} H={G * K} K={K} B={B} T={T} offset={offset} window={window}", flush=True)
+    got, ref = _prefill_case(6100 + case, dtype, B, G * K, K, D, T, offset, window)
+    assert max_abs(got, ref) <= tol(dtype)
+
+
 @pytest.mark.parametrize("window", [1, 64, 100, 1024])
 def test_prefill_sliding_window(window):
     got, ref = _prefill_case(window, torch.bfloat16, 1, 8, 1, 128, 700, 40, window)
