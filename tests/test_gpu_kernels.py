@@ -597,6 +597,34 @@ def test_decode_append_verify_steps(T, window, where):
             assert torch.equal(x, y), (dtype, D)
 
 
+@pytest.mark.parametrize("case", range(64))
+def test_random_decode_append_equals_two_calls(case):
+    """Seeded random steps with the cache write: forge_attn_decode_append against
+    forge_kv_append + forge_attn_decode, bit for bit (outputs and whole caches), over dtypes,
+    head dims 32-256, head groups 1-8, T up to 8, host / per-row / device positions,
+    windows, the values norm and the default or explicit chunks."""
+    rng = random.Random(5000 + case)
+    dtype = rng.choice(DTYPES)
+    D = rng.choice([32, 64, 128, 256])
+    G, K = rng.choice([1, 2, 3, 4, 8]), rng.choice([1, 2, 4])
+    T = rng.choice([1, 1, 2, 3, 5, 8])
+    B = rng.randint(1, 5)
+    where = rng.choice(["pos", "row_pos", "pos_dev"])
+    if where == "row_pos":
+        lens = [rng.randint(T, 1500) for _ in range(B)]
+    else:
+        lens = [rng.randint(T, 1500)] * B
+    window = rng.choice([0, 0, 1, 40])
+    chunk = rng.choice([0, 0, 256, 1024])
+    norm_v = rng.random() < 0.3
+    print(f"case {case}: {dtype} D={D} H={G * K} K={K} T={T} lens={lens} {where} window={window} "
+          f"chunk={chunk} norm_v={norm_v}", flush=True)
+    a, b, _ = _append_decode_pair(5100 + case, dtype, B, G * K, K, D, T, lens, window, where,
+                                  norm_v=norm_v, chunk=chunk)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
 def test_decode_append_against_the_oracle():
     """The fused step against the oracle: the keys the reference's KVCache.update would
     store after head_norm_rope (kv_cache.py:52-60, fused_ops.py:101-121), the values as
