@@ -489,6 +489,39 @@ def test_prefill_with_documents(dtype, D, layout, window):
     assert max_abs(got, ref) <= tol(dtype)
 
 
+@pytest.mark.parametrize("case", range(32))
+def test_random_document_prefill_against_oracle(case):
+    """Seeded random document layouts (every row cut into documents of random lengths,
+    single-token ones included), head dims, head groups and windows, against the oracle's
+    SDPA under the reference's same_doc mask."""
+    rng = random.Random(4000 + case)
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    D = rng.choice([64, 128, 256])
+    G, K = rng.choice([1, 2, 4]), rng.choice([1, 2])
+    B, T = rng.randint(1, 3), rng.randint(17, 600)
+    window = rng.choice([0, 0, 50])
+    layout = []
+    for _ in range(B):
+        cuts = sorted(rng.sample(range(1, T), rng.randint(0, min(8, T - 1))))
+        layout.append([e - b for b, e in zip([0] + cuts, cuts + [T])])
+    print(f"case {case}: {dtype} D={D} H={G * K} K={K} window={window} docs={layout}", flush=True)
+    g = gen(4100 + case)
+    docs = _doc_ids(layout)
+    H = G * K
+    q = randn(g, B, T, H, D, dtype=dtype).transpose(1, 2)
+    w = (1 + 0.1 * randn(g, D)).to(dtype)
+    kc = randn(g, B, K, T, D, dtype=dtype)
+    vc = randn(g, B, K, T, D, dtype=dtype)
+    c, s = tables(D, T, 1e4)
+    qn = oracle.head_norm_rope(q, w, 1e-6, c, s)
+    ref = oracle.sdpa(qn.float(), kc.float(), vc.float(), 0, window, scale_of(D),
+                      oracle.document_mask(docs)).transpose(1, 2)
+    got = ops().attn_prefill(q.to(DEV), kc.to(DEV), vc.to(DEV), scale=scale_of(D), window=window,
+                             q_weight=w.to(DEV), eps=1e-6, norm_q=True, cos=c.to(DEV), sin=s.to(DEV),
+                             doc_start=_doc_starts_of(docs).to(DEV)).cpu()
+    assert max_abs(got, ref) <= tol(dtype)
+
+
 def test_prefill_one_document_equals_plain_prefill():
     """Document starts all 0 (one document per row) change nothing, bit for bit."""
     g = gen(950)
