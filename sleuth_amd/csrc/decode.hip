@@ -41,6 +41,14 @@ namespace forge {
 constexpr int kSplitThreads = 256;
 constexpr int kSplitNK = FORGE_SPLIT_NK;  // keys per group per iteration
 constexpr int kMaxChunk = 1024;
+// ... but at least this many block iterations per unit: at head dim 32 (128 keys per
+// iteration in bf16) 1024 keys are only 8, and 2048-key chunks stream C4's lengths at 16 q /
+// 8 KV heads in 169 us against 189 us (at head dim 64, 16 iterations = 1024 keys, 2048 and
+// 4096 were slower: 321 and 330 against 315 us).
+constexpr int kMinMaxChunkIters = 16;
+__host__ __device__ constexpr int max_chunk_keys(int kpi) {
+  return kMaxChunk > kMinMaxChunkIters * kpi ? kMaxChunk : kMinMaxChunkIters * kpi;
+}
 constexpr float kRescaleLog2 = 8.0f;  // lazy rescale: weights stay <= 2^8
 // Register buffers of the K/V pipeline (loads run PF - 1 iterations ahead): deeper where
 // few query rows leave the registers for it. Measured on C4-shaped ragged decode: PF 4
@@ -1541,7 +1549,7 @@ static int auto_chunk(int dtype, int B, int /*T*/, int H, int K, int D, int64_t 
   int chunk = kpi;
   const int64_t len = max_kv_len > 0 ? max_kv_len : 1;
   const int ncu = device_cus();
-  while (chunk * 2 <= kMaxChunk &&
+  while (chunk * 2 <= max_chunk_keys(kpi) &&
          (chunk < 4 * kpi || pairs * ((len + chunk * 2 - 1) / (chunk * 2)) >= ncu))
     chunk *= 2;
   return chunk;
@@ -1587,7 +1595,7 @@ static int uniform_chunk(int dtype, int B, int H, int K, int D, int64_t max_kv_l
   // capacity, which a row may be far from reaching, so the chunk stays at most as long as
   // the general rule's (a capacity of 32768 at C2's 64 pairs would otherwise give 8192-key
   // chunks, one unit per row of 2049 keys: 30.9 us per call against 19.9 us).
-  if (pairs < ncu && best > kMaxChunk) best = kMaxChunk;
+  if (pairs < ncu && best > max_chunk_keys(kpi)) best = max_chunk_keys(kpi);
   return best > INT_MAX ? INT_MAX / kpi * kpi : (int)best;
 }
 
