@@ -22,7 +22,9 @@ of head_norm_rope + cache.update + SDPA):
       to forge_attn_prefill_docs, which takes each query's first visible key.
     The output comes back as [B, T, H, hd], the layout o_proj reads.
   * torch (CPU, training, FlexAttention block masks and other document masks, the
-    pattern tap, or SLEUTH_AMD_NO_HIP=1): the reference's eager code, unchanged in meaning.
+    pattern tap, or SLEUTH_AMD_NO_HIP=1): the reference's eager code, unchanged in meaning;
+    a BlockMask goes to flex_attention with the reference's NotImplementedError for a
+    pattern tap, a window or a cached prefix (attention.py:142-149).
 If a GPU tensor would take the HIP path and the library is missing or fails its
 first-use self-check, forward raises: there is no silent fallback.
 """
@@ -52,6 +54,29 @@ def hip_disabled() -> bool:
     return os.environ.get("SLEUTH_AMD_NO_HIP") == "1"
 
 
+_FLEX_LIMITS = ("FlexAttention document masks are for training: no attention taps, sliding windows "
+                "or KV cache")
+
+
+def doc_block_mask(doc_ids: torch.Tensor):
+    """[B, T] document numbers -> a FlexAttention BlockMask that is causal and within one
+    document (the reference's doc_block_mask, attention.py:54-64): built once per batch and
+    shared by every layer; the torch path passes it to flex_attention."""
+    from torch.nn.attention.flex_attention import create_block_mask
+
+    B, T = doc_ids.shape
+
+    def mask_mod(b, h, qi, ki):
+        return (ki <= qi) & (doc_ids[b, ki] == doc_ids[b, qi])
+
+    return create_block_mask(mask_mod, B, None, T, T, device=doc_ids.device)
+
+
+def _is_block_mask(m) -> bool:
+    """A FlexAttention BlockMask (anything but a tensor) in place of the bool same_doc mask."""
+    return m is not None and not isinstance(m, torch.Tensor)
+
+
 _DOC_STARTS: dict = {}   # the last mask's doc starts: one mask serves every layer of a pass
 
 
@@ -65,7 +90,10 @@ def _doc_starts(same_doc, B: int, T: int) -> torch.Tensor | None:
     if not (isinstance(m, torch.Tensor) and m.dtype == torch.bool and m.is_cuda and m.dim() == 4
             and m.shape[1] == 1 and tuple(m.shape[2:]) == (T, T) and m.shape[0] in (1, B)):
         return None
-    hit = _DOC_STARTS.get("last")
+    # inference tensors keep no version counter, so a mask made under inference_mode is
+    # read again at every layer rather than trusted unchanged
+    cached = not m.is_inference()
+    hit = _DOC_STARTS.get("last") if cached else None
     if hit is not None and hit[0]() is m and hit[1] == (m._version, B):
         return hit[2]
     vis = m[:, 0] & torch.ones(T, T, dtype=torch.bool, device=m.device).tril()
@@ -74,7 +102,8 @@ def _doc_starts(same_doc, B: int, T: int) -> torch.Tensor | None:
     run = (vis.sum(-1) == pos - start + 1).all() & vis.diagonal(dim1=-2, dim2=-1).all()
     run &= (start[:, 1:] >= start[:, :-1]).all()
     res = start.to(torch.int32).expand(B, T).contiguous() if bool(run) else None
-    _DOC_STARTS["last"] = (weakref.ref(m), (m._version, B), res)
+    if cached:
+        _DOC_STARTS["last"] = (weakref.ref(m), (m._version, B), res)
     return res
 
 
@@ -327,6 +356,8 @@ class Attention(nn.Module):
             q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
         q, k = self.tap_q(q), self.tap_k(k)
         if cache is not None and getattr(cache, "ragged", False) and not getattr(cache, "static", False):
+            if _is_block_mask(same_doc):
+                raise NotImplementedError(_FLEX_LIMITS)
             return self._ragged_torch(q, k, v, cache, same_doc)
         if cache is not None:
             k, v = cache.update(self.layer_idx, k, v)
@@ -336,6 +367,16 @@ class Attention(nn.Module):
             kwargs = {"enable_gqa": True} if self.n_kv != self.n_heads else {}
             return F.scaled_dot_product_attention(q, k, v, attn_mask=cache.attn_mask(self.window),
                                                   scale=self.scale, **kwargs)
+        if _is_block_mask(same_doc):
+            # FlexAttention document mask (doc_block_mask, attention.py:54-64): the reference
+            # hands it to flex_attention and allows no pattern tap, window or cached prefix
+            # (attention.py:142-149)
+            if tap_active(self.tap_pattern) or self.window or offset:
+                raise NotImplementedError(_FLEX_LIMITS)
+            from torch.nn.attention.flex_attention import flex_attention
+
+            return flex_attention(q, k, v, block_mask=same_doc, scale=self.scale,
+                                  enable_gqa=self.n_kv != self.n_heads)
         if tap_active(self.tap_pattern):
             return self._explicit(q, k, v, offset, same_doc)
         return self._fused(q, k, v, offset, same_doc)

@@ -318,6 +318,54 @@ def test_document_mask_on_cpu_takes_the_torch_path():
     assert att._doc_starts(m, 1, 5) is None
 
 
+def test_flex_block_mask_matches_the_bool_document_mask():
+    """A FlexAttention BlockMask from doc_block_mask gives the bool same_doc mask's output
+    (attention.py:142-149 against 184-186); a pattern tap, a window or a cached prefix raise
+    NotImplementedError as the reference's branch does."""
+    pytest.importorskip("torch.nn.attention.flex_attention")
+    import warnings
+
+    from sleuth_amd.attention import doc_block_mask
+
+    torch.manual_seed(5)
+    doc_ids = torch.tensor([[0] * 9 + [1] * 14 + [2] * 9, [0] * 20 + [1] * 12])
+    B, T = doc_ids.shape
+    cfg = ModelConfig(vocab_size=10, d_model=64, n_heads=4, n_kv_heads=2, qk_norm=True, n_layers=1)
+    a = Attention(cfg, 0).eval()
+    x = torch.randn(B, T, 64)
+    cos, sin = oracle.rope_tables(16, T, 1e4)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")      # flex_attention's eager-mode notice
+        bm = doc_block_mask(doc_ids)
+        with torch.no_grad():
+            want = a(x, cos, sin, same_doc=oracle.document_mask(doc_ids))
+            got = a(x, cos, sin, same_doc=bm)
+        assert a.last_path == "torch"
+        torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-4)
+        # the mask really is block-diagonal: the first document's output ignores the rest
+        x2 = x.clone()
+        x2[:, 9:] = torch.randn(B, T - 9, 64)
+        with torch.no_grad():
+            torch.testing.assert_close(a(x2, cos, sin, same_doc=bm)[0, :9], got[0, :9], atol=1e-5, rtol=1e-4)
+
+        assign_tap_names(a)
+        with torch.no_grad(), listen(a, {"pattern": lambda n, t: t}):
+            with pytest.raises(NotImplementedError):
+                a(x, cos, sin, same_doc=bm)
+        w = ModelConfig(vocab_size=10, d_model=64, n_heads=4, n_kv_heads=2, n_layers=1,
+                        layer_types=["sliding"], sliding_window=4)
+        with torch.no_grad(), pytest.raises(NotImplementedError):
+            Attention(w, 0).eval()(x, cos, sin, same_doc=bm)
+        cache = KVCache([(2, 16)], B, T + 8, "cpu", torch.float32)
+        with torch.no_grad():
+            cfg1 = ModelConfig(vocab_size=10, d_model=64, n_heads=4, n_kv_heads=2, n_layers=1)
+            a1 = Attention(cfg1, 0).eval()
+            a1(x[:, :4], cos[:4], sin[:4], cache=cache)
+            cache.advance(4)
+            with pytest.raises(NotImplementedError):
+                a1(x[:, 4:], cos[4:], sin[4:], cache=cache, same_doc=bm)
+
+
 @pytest.mark.parametrize("sliding,n_past", [(False, 1), (False, 40), (True, 5), (True, 40)])
 def test_drafter_attention_module_torch_path(sliding, n_past):
     """The MTP drafter's attention (mtp.py:73-92) on the CPU: RMSNorm then RoPE at position
