@@ -379,6 +379,69 @@ def cpu_baseline_prefill(B, T, H, K, D) -> dict:
 
 
 # ----------------------------------------------------------------------------- main
+# ----------------------------------------------------------------------------- output check
+CHECK_TOL = 2e-2   # bf16 max-abs bound (north star)
+
+
+def _norm_rope_fp32(x, w, cos, sin, eps=1e-6):
+    """RMSNorm with gain w, then NEOX RoPE, in fp32 with one rounding to x's dtype: the
+    arithmetic of the fused q/k load (reference fused_ops.py:53-85), as plain torch."""
+    xf = x.float()
+    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w
+    h = y.shape[-1] // 2
+    return (y * cos + torch.cat([-y[..., h:], y[..., :h]], -1) * sin).to(x.dtype)
+
+
+def check_decode(wl: "DecodeWorkload") -> float:
+    """The last step's own output against fp32 torch attention on the GPU, for the longest
+    and the shortest row, over the cache the step wrote (the new key at L - 1 must be the
+    normalised, rotated one). Returns the max-abs error; raises if it exceeds CHECK_TOL."""
+    assert wl.T == 1
+    G = wl.H // wl.K
+    i = (wl.layer - 1) % len(wl.k_caches)
+    kc, vc = wl.k_caches[i], wl.v_caches[i]
+    worst = 0.0
+    for b in (max(range(wl.B), key=lambda r: wl.lens[r]), min(range(wl.B), key=lambda r: wl.lens[r])):
+        L = wl.lens[b]
+        c, s_ = wl.cos[b, 0], wl.sin[b, 0]
+        kn = _norm_rope_fp32(wl.k[b, :, 0], wl.wk, c, s_).float()
+        err_k = (kc[b, :, L - 1].float() - kn).abs().max().item()
+        if not err_k <= CHECK_TOL * (1 + kn.abs().max().item()):
+            raise RuntimeError(f"bench check: row {b}: the new key in the cache is off by {err_k:.3e}")
+        qn = _norm_rope_fp32(wl.q[b, :, 0], wl.wq, c, s_).float().view(wl.K, G, wl.D)
+        k, v = kc[b, :, :L].float(), vc[b, :, :L].float()
+        p = (torch.matmul(qn, k.transpose(1, 2).contiguous()) * wl.scale).softmax(-1)
+        y = torch.matmul(p, v).reshape(wl.H, wl.D)
+        worst = max(worst, (wl.out[b, 0].float() - y).abs().max().item())
+    if not worst <= CHECK_TOL:
+        raise RuntimeError(f"bench check: decode output off by {worst:.3e} (bound {CHECK_TOL})")
+    return worst
+
+
+def check_prefill(pf: "PrefillWorkload", b: int = 0) -> float:
+    """The last prefill's own output for batch row b (its first 64 and last 128 queries,
+    every head) against fp32 causal attention in torch on the GPU over the cache the append
+    wrote. Returns the max-abs error; raises if it exceeds CHECK_TOL."""
+    G = pf.H // pf.K
+    idx = torch.cat([torch.arange(64), torch.arange(pf.T - 128, pf.T)]).to(pf.out.device)
+    qn = _norm_rope_fp32(pf.q[b][:, idx], pf.wq, pf.cos[idx], pf.sin[idx]).float()     # [H, n, D]
+    k = pf.kc[b].float().repeat_interleave(G, 0)                                        # [H, T, D]
+    v = pf.vc[b].float().repeat_interleave(G, 0)
+    s = torch.matmul(qn, k.transpose(1, 2).contiguous()) * pf.scale                     # [H, n, T]
+    s = s.masked_fill(torch.arange(pf.T, device=s.device)[None, None, :] > idx[None, :, None], float("-inf"))
+    y = torch.matmul(s.softmax(-1), v)                                                  # [H, n, D]
+    worst = (pf.out[b][idx].float() - y.transpose(0, 1)).abs().max().item()
+    if not worst <= CHECK_TOL:
+        raise RuntimeError(f"bench check: prefill output off by {worst:.3e} (bound {CHECK_TOL})")
+    return worst
+
+
+def mean_step_bytes(wl: "DecodeWorkload", lo: int = 1024, hi: int = 32768) -> float:
+    """Algorithmic bytes of a step whose rows have the mean length of U[lo, hi]."""
+    s = torch.finfo(wl.dtype).bits // 8
+    return wl.step_bytes() + 2 * wl.K * wl.D * s * (wl.B * (lo + hi) / 2 - sum(wl.lens))
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -425,6 +488,9 @@ def main() -> int:
     print(f"[bench] C4 step {t_step * 1e6:.1f} us ({step_gbs:.0f} GB/s), attention call "
           f"{t_attn * 1e6:.1f} us ({attn_gbs:.0f} GB/s), two-call step {t_two * 1e6:.1f} us",
           file=sys.stderr, flush=True)
+    wl.step()   # the timed call once more; its output is checked below
+    torch.cuda.synchronize()
+    err_decode = check_decode(wl)
 
     # ---- C3 prefill
     pf = PrefillWorkload(4, 4096, 16, 8, 128, 1e6, dt, dev)
@@ -436,6 +502,10 @@ def main() -> int:
     p_step_tflops = pf.flops() / t_pstep / 1e12
     print(f"[bench] C3 prefill step {t_pstep * 1e6:.1f} us ({p_step_tflops:.0f} TFLOP/s), attention kernel "
           f"{t_pattn * 1e6:.1f} us ({p_tflops:.0f} TFLOP/s)", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    err_prefill = check_prefill(pf)
+    print(f"[bench] outputs checked against fp32 torch: decode max-abs {err_decode:.2e} (longest and "
+          f"shortest rows), prefill max-abs {err_prefill:.2e}", file=sys.stderr, flush=True)
     gemm = gemm_tflops(dev)
     print(f"[bench] bf16 8192^3 library GEMM {gemm:.0f} TFLOP/s", file=sys.stderr, flush=True)
     sdpa = sdpa_reference(dev)
@@ -460,6 +530,11 @@ def main() -> int:
                    "global_batch": wl.B, "kv_tokens": sum(lens), "chunk": wl.chunk,
                    "parallelism": "single GPU"},
         "decode_tokens_per_s": round(tok_s, 1),
+        # this seed's draw has sum L = 948,477 keys, 12% below the distribution's mean of
+        # 1,081,344; tokens/s at the same GB/s for a batch of the mean size
+        "decode_tokens_per_s_at_mean_lengths": round(tok_s * wl.step_bytes() / mean_step_bytes(wl), 1),
+        # the timed calls' own outputs against fp32 torch attention on the GPU (max-abs)
+        "output_check": {"decode_max_abs": err_decode, "prefill_max_abs": err_prefill, "bound": CHECK_TOL},
         "decode_attention_call_us": round(t_attn * 1e6, 2),
         # the same step as forge_kv_append + forge_attn_decode (two launches, and the
         # persistent grid's ticket reset and the combine), for comparison

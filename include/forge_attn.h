@@ -126,6 +126,10 @@ int forge_attn_decode(int dtype, int B, int T, int H, int K, int D, const void* 
  * which saves the small kernel that otherwise zeroes them; every call leaves them zero, so a
  * workspace cleared once before its first use keeps the promise for the calls that follow it
  * on one stream.
+ * With device-held positions (row_pos or pos_dev), max_kv_len must be at least base_b + T
+ * for every row: the launch covers the keys below max_kv_len only, so a new key or value at
+ * a position at or past max_kv_len is not written (forge_kv_append writes up to max_len).
+ * With pos0 the call raises max_kv_len to pos0 + T itself.
  */
 #define FORGE_WS_ZEROED 1 /* ws_flags: the workspace's first 4 bytes hold zero */
 int forge_attn_decode_append(int dtype, int B, int T, int H, int K, int D, const void* q,
@@ -164,9 +168,11 @@ int forge_attn_decode_noalloc(int dtype, int B, int T, int H, int K, int D, cons
                               void* stream);
 
 /* Keys per split for a row span of max_kv_len keys (pure host function): the rule for
- * per-row positions (row_pos), whose ragged rows need chunks short enough to balance; at
- * most 1024 keys (the MFMA path on more than 512 rows: 512). T is accepted for the
- * signature but does not enter, so decode and verify steps of one layer agree. */
+ * per-row positions (row_pos), whose ragged rows need chunks short enough to balance. The
+ * cap is max(1024, 16 block iterations) keys: 1024 for most shapes, 2048 at D 32 in
+ * bf16/fp16 (128 keys per block iteration); the MFMA path on more than 512 rows takes at
+ * most 512. T is accepted for the signature but does not enter, so decode and verify steps
+ * of one layer agree. Size buffers with forge_attn_decode_workspace_bytes, not the cap. */
 int forge_attn_decode_chunk(int dtype, int B, int T, int H, int K, int D, int64_t max_kv_len);
 
 /* Keys per split for calls whose rows all start at one position (pos0 or pos_dev, no

@@ -1,9 +1,10 @@
 """Attention hyperparameters (the attention fields of the reference's ModelConfig).
 
-Mirrors sleuth/forge/model/config.py: ModelConfig fields used by attention (24-63),
-the per-layer AttnSpec (180-187) and attn_spec(i) (142-147), with the same validation
-of head counts, head sizes and layer kinds (96-137). 0 means "use the default" for
-head_size / n_kv_heads, as in the reference.
+The fields follow sleuth/forge/model/config.py's ModelConfig (24-63), so the module also
+accepts the reference's own config object; AttnSpec and attn_spec(i) give each layer's
+shape as config.py:142-147,180-187 define it (sliding layers take the swa_* overrides).
+0 means "use the default" for head_size / n_kv_heads, as in the reference. The checks
+below only reject what this package's module and harness cannot build.
 """
 
 from __future__ import annotations
@@ -54,33 +55,29 @@ class ModelConfig:
     init_std: float = 0.02
 
     def __post_init__(self):
-        if not self.head_size and self.d_model % self.n_heads:
-            raise ValueError(f"d_model ({self.d_model}) must be divisible by n_heads ({self.n_heads})")
-        if self.kv_heads <= 0 or self.n_heads % self.kv_heads:
-            raise ValueError(f"n_heads ({self.n_heads}) must be a multiple of n_kv_heads ({self.kv_heads})")
-        if self.layer_types and len(self.layer_types) != self.n_layers:
-            raise ValueError(f"layer_types has {len(self.layer_types)} entries for {self.n_layers} layers")
-        if any(t not in ("full", "sliding") for t in self.layer_types):
-            raise ValueError(f"layer_types entries must be 'full' or 'sliding', got {sorted(set(self.layer_types))}")
-        if "sliding" in self.layer_types and self.sliding_window <= 0:
-            raise ValueError("sliding layers need sliding_window > 0")
-        if self.shared_layers:
-            src = self.shared_layers
-            if len(src) != self.n_layers:
-                raise ValueError(f"shared_layers has {len(src)} entries for {self.n_layers} layers")
-            for i, j in enumerate(src):
-                if not 0 <= j <= i or src[j] != j:
-                    raise ValueError(f"layer {i} cannot share layer {j}'s weights: the source must be "
-                                     "an earlier (or the same) layer that is not shared itself")
-        if self.pos_type not in ("rope", "none", "learned"):
-            raise ValueError(f"pos_type must be one of ('rope', 'none', 'learned'), got {self.pos_type!r}")
-        for spec in {self.attn_spec(i) for i in range(self.n_layers)}:
-            if spec.kv_heads <= 0 or self.n_heads % spec.kv_heads:
-                raise ValueError(f"n_heads ({self.n_heads}) must be a multiple of the KV heads ({spec.kv_heads})")
-            if spec.head_dim % 2 and self.pos_type == "rope":
-                raise ValueError("RoPE needs an even head_dim")
-            if self.rope_dim and (self.rope_dim % 2 or self.rope_dim > spec.head_dim):
-                raise ValueError(f"rope_dim ({self.rope_dim}) must be even and at most the head size")
+        """Rejects the shapes the attention module and the harness cannot build."""
+        n = self.n_layers
+        kinds = self.layer_types or ["full"] * n
+        bad = [
+            (not self.head_size and self.d_model % self.n_heads, "d_model is not a multiple of n_heads"),
+            (len(kinds) != n, "layer_types needs one entry per layer"),
+            (not set(kinds) <= {"full", "sliding"}, "layer_types entries are 'full' or 'sliding'"),
+            ("sliding" in kinds and self.sliding_window <= 0, "sliding layers need sliding_window > 0"),
+            (self.pos_type not in ("rope", "none", "learned"), "pos_type is 'rope', 'none' or 'learned'"),
+            (bool(self.shared_layers) and len(self.shared_layers) != n, "shared_layers needs one entry per layer"),
+        ]
+        if not bad[1][0]:
+            specs = [self.attn_spec(i) for i in range(n)]
+            for s in specs:
+                bad += [(s.kv_heads <= 0 or self.n_heads % s.kv_heads, "n_heads is not a multiple of the KV heads"),
+                        (self.pos_type == "rope" and s.head_dim % 2, "RoPE needs an even head size"),
+                        (self.rope_dim % 2 or self.rope_dim > s.head_dim, "rope_dim must be even and fit the head")]
+            # a shared layer points at an earlier (or the same) layer that owns its weights
+            bad += [(not (0 <= j <= i and self.shared_layers[j] == j), f"layer {i} cannot share layer {j}")
+                    for i, j in enumerate(self.shared_layers) if len(self.shared_layers) == n]
+        for failed, why in bad:
+            if failed:
+                raise ValueError(f"bad attention config: {why}")
 
     def layer_type(self, i: int) -> str:
         return self.layer_types[i] if self.layer_types else "full"

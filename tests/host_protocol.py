@@ -60,42 +60,42 @@ class HostKVCache:
 
 
 class HostStaticKVCache(HostKVCache):
+    """The static (graph) members only; the step's positions and masks are made on first
+    use after new_step() and kept until the next one."""
+
     def __init__(self, shapes, batch, max_len, device, dtype, tokens_per_step=1):
         super().__init__(shapes, batch, max_len, device, dtype)
         self.static = False
         self.length = max_len
         self.pos_t = torch.zeros(1, dtype=torch.long, device=device)
-        self._kpos = torch.arange(max_len, device=device)
         self.tokens_per_step = tokens_per_step
-        self._qoff = torch.arange(tokens_per_step, device=device)
-        self._masks = {}
-        self._pos = None
+        self.new_step()
+
+    def new_step(self, positions=None):
+        self._step = {"positions": positions}
 
     @property
     def positions(self):
-        if self._pos is None:
-            self._pos = self.pos_t + self._qoff
-        return self._pos
+        if self._step["positions"] is None:
+            self._step["positions"] = self.pos_t + torch.arange(self.tokens_per_step, device=self.pos_t.device)
+        return self._step["positions"]
 
     def update(self, layer, k_new, v_new):
         if not self.static:
             return super().update(layer, k_new, v_new)
-        self.k[layer].index_copy_(2, self.positions, k_new.to(self.k[layer].dtype))
-        self.v[layer].index_copy_(2, self.positions, v_new.to(self.v[layer].dtype))
+        for cache, new in ((self.k[layer], k_new), (self.v[layer], v_new)):
+            cache.index_copy_(2, self.positions, new.to(cache.dtype))
         return self.k[layer][:, :, :self.length], self.v[layer][:, :, :self.length]
 
     def attn_mask(self, window=0):
-        if window not in self._masks:
-            kpos = self._kpos[:self.length][None, :]
-            qpos = self.positions[:, None]
-            ok = kpos <= qpos
+        if window not in self._step:
+            q = self.positions[:, None]
+            k = torch.arange(self.length, device=q.device)[None, :]
+            ok = k <= q
             if window:
-                ok = ok & (qpos - kpos < window)
-            self._masks[window] = ok[None, None]
-        return self._masks[window]
-
-    def new_step(self, positions=None):
-        self._masks, self._pos = {}, positions
+                ok &= q - k < window
+            self._step[window] = ok[None, None]
+        return self._step[window]
 
     def advance(self, n):
         if not self.static:

@@ -53,6 +53,12 @@ def test_host_only_functions():
     # (up to 512 rows), 512 on the dense grid beyond it
     assert lib.forge_attn_decode_chunk(_lib.BF16, 64, 1, 32, 8, 128, 32768) == 1024
     assert lib.forge_attn_decode_chunk(_lib.BF16, 600, 1, 32, 8, 128, 32768) == 512
+    # the cap is max(1024, 16 block iterations): 2048 keys at head dim 32 in bf16/fp16 (128
+    # keys per iteration), 1024 at head dim 64 and above and in fp32
+    assert lib.forge_attn_decode_chunk(_lib.BF16, 64, 1, 16, 8, 32, 32768) == 2048
+    assert lib.forge_attn_decode_chunk(_lib.F16, 64, 1, 16, 8, 32, 32768) == 2048
+    assert lib.forge_attn_decode_chunk(_lib.BF16, 64, 1, 16, 8, 64, 32768) == 1024
+    assert lib.forge_attn_decode_chunk(_lib.F32, 64, 1, 16, 8, 32, 32768) == 1024
 
 
 def test_uniform_chunk_rule():

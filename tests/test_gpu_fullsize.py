@@ -162,6 +162,52 @@ def test_c4_ragged_decode_full_size(chunk):
     assert worst <= 2e-2
 
 
+def test_c4_bench_call_at_the_bench_workload():
+    """The headline's own call at its own workload: bench.DecodeWorkload for C4 (seed 0, 64
+    rows of U[1024, 32768] keys, 1024-key chunks on the persistent grid), its step() --
+    forge_attn_decode_append on a workspace cleared once, FORGE_WS_ZEROED -- run twice in a
+    row as the timed loop runs it. The new rows it writes equal forge_kv_append's and its
+    output equals forge_kv_append + forge_attn_decode bit for bit (at this size, up to 32
+    chunks per row into the combine); the longest and the shortest rows against the oracle."""
+    import bench
+
+    lens = bench.c4_lengths(0)
+    H, K, D = 16, 8, 128
+    wl = bench.DecodeWorkload(lens, H, K, D, 1e6, BF, torch.device(DEV), seed=0)
+    assert wl.pos is None and wl.chunk == 1024 and max(lens) > 31 * 1024
+    wl.append()                                     # as bench.main does before timing
+    kc, vc = wl.k_caches[0], wl.v_caches[0]
+    rows = torch.tensor([L - 1 for L in lens], device=DEV)
+    b_idx, h_idx = torch.arange(64, device=DEV)[:, None], torch.arange(K, device=DEV)[None, :]
+    k_new, v_new = kc[b_idx, h_idx, rows[:, None]].clone(), vc[b_idx, h_idx, rows[:, None]].clone()
+    wl.attend()                                     # the two-call step's attention
+    two = wl.out.clone()
+    kc[b_idx, h_idx, rows[:, None]] = POISON        # the fused step must write them itself
+    vc[b_idx, h_idx, rows[:, None]] = POISON
+    wl.step()
+    first = wl.out.clone()
+    wl.step()                                       # the workspace as the previous call left it
+    torch.cuda.synchronize()
+    assert torch.equal(kc[b_idx, h_idx, rows[:, None]], k_new) and torch.equal(vc[b_idx, h_idx, rows[:, None]], v_new)
+    assert torch.equal(first, two), "forge_attn_decode_append differs from the two calls"
+    assert torch.equal(wl.out, first), "the second call on the reused workspace differs"
+    q = wl.q.cpu()
+    order = sorted(range(64), key=lambda b: lens[b])
+    worst = 0.0
+    for b in (order[0], order[-1]):
+        L = lens[b]
+        c, s_ = wl.cos[b].cpu(), wl.sin[b].cpu()                         # [1, D]
+        qn = oracle.head_norm_rope(q[b:b + 1], wl.wq.cpu(), 1e-6, c, s_).float()
+        kn = oracle.head_norm_rope(wl.k[b:b + 1].cpu(), wl.wk.cpu(), 1e-6, c, s_)
+        assert max_abs(kc[b, :, L - 1], kn[0, :, 0]) <= 2e-2
+        ref = oracle.sdpa(qn, kc[b:b + 1, :, :L].float().cpu(), vc[b:b + 1, :, :L].float().cpu(), L - 1, 0,
+                          wl.scale).transpose(1, 2)
+        worst = max(worst, max_abs(wl.out[b:b + 1].float().cpu(), ref))
+    print(f"C4 bench call: rows {order[0]} (L {lens[order[0]]}) and {order[-1]} (L {lens[order[-1]]}) "
+          f"max-abs {worst:.3e}", flush=True)
+    assert worst <= 2e-2
+
+
 def test_bf16_precision_kat_head_dim_256():
     """The reference's bf16 KAT (tests/test_gpu.py:186-198): hd 256, T 256, theta 1e6,
     x = 3 N(0,1), gain 1 + 0.3 N(0,1). Exact = fp32 RMSNorm + RoPE; eager rounds after the

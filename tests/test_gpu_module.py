@@ -298,6 +298,18 @@ def test_document_mask_on_the_hip_path(hd, monkeypatch):
         gapped[0, 250:] = 0                         # document 0 again, after documents 1-3
         a(x, cos, sin, same_doc=oracle.document_mask(gapped))
         assert a.last_path == "torch"
+    # under inference_mode the mask is an inference tensor (no version counter): its starts
+    # are read again at each call, so a mask changed in place is seen
+    with torch.inference_mode():
+        m_inf = oracle.document_mask(docs)
+        got_inf = a(x, cos, sin, same_doc=m_inf).float()
+        assert a.last_path == "hip-prefill-docs"
+        assert torch.equal(got_inf, got)
+        m_inf.copy_(oracle.document_mask(torch.zeros_like(docs)))   # one document per row
+        one = a(x, cos, sin, same_doc=m_inf).float()
+        assert a.last_path == "hip-prefill-docs"
+        plain = a(x, cos, sin).float()
+        assert torch.equal(one, plain)
 
 
 @pytest.mark.parametrize("host_cache", [False, True])
