@@ -115,6 +115,71 @@ template <int N> __device__ __forceinline__ void wait_vm() {
   else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
 }
 
+// Q rows of one wave as MFMA B operands: load, fused RMSNorm + RoPE (fp32, one rounding).
+// Lane (n, hi) holds channels 16s + 8hi + e of query i_q; gains and RoPE rows come in
+// 16-byte loads.
+template <typename T, int D>
+__device__ __forceinline__ void load_q(const PrefillParams& p, int b, int h, int i_q, bool valid_q,
+                                       int hi, typename Mfma<T>::vec (&qreg)[D / 16]) {
+  constexpr int KSTEPS = D / 16;
+  float qf[KSTEPS][8];
+  const T* src = static_cast<const T*>(p.q) + b * p.sqb + h * p.sqh + (int64_t)i_q * p.sqt;
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s) {
+    if (valid_q) {
+      unpack16<T>(load16(src + 16 * s + 8 * hi), qf[s]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[s][e] = 0.0f;
+    }
+  }
+  if (p.flags & FORGE_NORM_QK) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += qf[s][e] * qf[s][e];
+    ss += __shfl_xor(ss, 32, kWave);
+    const float rs = rsqrtf(ss / (float)D + p.eps);
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[s][e] *= rs;
+    if (p.qw) {
+      float w[KSTEPS][8];
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) load_f32x8(p.qw + 16 * s + 8 * hi, w[s]);
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[s][e] *= w[s][e];
+    }
+  }
+  if ((p.flags & FORGE_ROPE) && valid_q) {
+    const float* cr = p.cos + (int64_t)i_q * p.cst;
+    const float* sr = p.sin + (int64_t)i_q * p.cst;
+#pragma unroll
+    for (int s = 0; s < KSTEPS / 2; ++s) {
+      const int x = 16 * s + 8 * hi;  // first-half channels x..x+7; partners x + D/2
+      float c1[8], s1[8], c2[8], s2[8];
+      load_f32x8(cr + x, c1);
+      load_f32x8(sr + x, s1);
+      load_f32x8(cr + x + D / 2, c2);
+      load_f32x8(sr + x + D / 2, s2);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a = qf[s][e], z = qf[s + KSTEPS / 2][e];
+        qf[s][e] = a * c1[e] - z * s1[e];
+        qf[s + KSTEPS / 2][e] = z * c2[e] + a * s2[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qreg[s][e] = from_f32<T>(qf[s][e]);
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(Tile<D>::WAVES * 64) __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2)))
 void prefill_kernel(PrefillParams p) {
@@ -233,67 +298,9 @@ void prefill_kernel(PrefillParams p) {
   for (int j = 1; j < TL::STAGES - 1; ++j)
     if (kt_begin + j <= kt_end) issue(kt_begin + j, j);
 
-  // ---- Q: load, fused RMSNorm + RoPE, one rounding, kept as MFMA B operands. Lane
-  // (n, hi) holds channels 16s + 8hi + e; gains and RoPE rows come in 16-byte loads.
+  // ---- Q: load, fused RMSNorm + RoPE, one rounding, kept as MFMA B operands.
   V8 qreg[KSTEPS];
-  {
-    float qf[KSTEPS][8];
-    const T* src = static_cast<const T*>(p.q) + b * p.sqb + h * p.sqh + (int64_t)i_q * p.sqt;
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      if (valid_q) {
-        unpack16<T>(load16(src + 16 * s + 8 * hi), qf[s]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qf[s][e] = 0.0f;
-      }
-    }
-    if (p.flags & FORGE_NORM_QK) {
-      float ss = 0.0f;
-#pragma unroll
-      for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += qf[s][e] * qf[s][e];
-      ss += __shfl_xor(ss, 32, kWave);
-      const float rs = rsqrtf(ss / (float)D + p.eps);
-#pragma unroll
-      for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qf[s][e] *= rs;
-      if (p.qw) {
-        float w[KSTEPS][8];
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) load_f32x8(p.qw + 16 * s + 8 * hi, w[s]);
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) qf[s][e] *= w[s][e];
-      }
-    }
-    if ((p.flags & FORGE_ROPE) && valid_q) {
-      const float* cr = p.cos + (int64_t)i_q * p.cst;
-      const float* sr = p.sin + (int64_t)i_q * p.cst;
-#pragma unroll
-      for (int s = 0; s < KSTEPS / 2; ++s) {
-        const int x = 16 * s + 8 * hi;  // first-half channels x..x+7; partners x + D/2
-        float c1[8], s1[8], c2[8], s2[8];
-        load_f32x8(cr + x, c1);
-        load_f32x8(sr + x, s1);
-        load_f32x8(cr + x + D / 2, c2);
-        load_f32x8(sr + x + D / 2, s2);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float a = qf[s][e], z = qf[s + KSTEPS / 2][e];
-          qf[s][e] = a * c1[e] - z * s1[e];
-          qf[s + KSTEPS / 2][e] = z * c2[e] + a * s2[e];
-        }
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qreg[s][e] = from_f32<T>(qf[s][e]);
-  }
+  load_q<T, D>(p, b, h, i_q, valid_q, hi, qreg);
 
   // this wave's query span (tile skipping and the mask-free fast path); positions fit
   // in 32 bits (host check)
