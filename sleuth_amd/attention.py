@@ -7,12 +7,12 @@ signature forward(x, cos, sin, cache=None, same_doc=None) -> [B, T, d].
 
 Paths (the reference's own dispatch, attention.py:109-153, with the HIP kernels in place
 of head_norm_rope + cache.update + SDPA):
-  * HIP (GPU inference: no grad, dtype fp32/bf16/fp16, head dim 32/64/128/256, nobody
-    listening on attn.pattern; a document mask only as below):
+  * HIP (GPU inference: no grad, dtype fp32/bf16/fp16, head dim 32/64/128/256, and 512 in
+    bf16/fp16, nobody listening on attn.pattern; a document mask only as below):
       k norm + RoPE (+ v norm), written into the cache at pos / pos_t / per-row
       lengths (with partial RoPE, norm and RoPE run in torch as the reference's eager
       code does, and the kernels take q and k as they are), then attention:
-      T > 16, bf16/fp16, head dim 64/128/256: forge_kv_append, then forge_attn_prefill
+      T > 16, bf16/fp16, head dim 64-512:     forge_kv_append, then forge_attn_prefill
                         (MFMA flash) with the q norm + RoPE in its q load;
       otherwise         forge_attn_decode_append: the cache write and the split-K
                         attention (decode, verify, static steps, fp32, other head sizes)
@@ -45,8 +45,14 @@ from .rope import apply_rope
 from .taps import make_tap, tap_active
 
 DECODE_MAX_T = 16
-_HIP_HEAD_DIMS = (32, 64, 128, 256)
+_HIP_HEAD_DIMS = (32, 64, 128, 256, 512)   # 512 (Gemma 4's full layers) in bf16/fp16 only
 _HIP_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def hip_shape_ok(dtype: torch.dtype, head_dim: int) -> bool:
+    """The kernels take this dtype and head dim (a 512-wide key row must be 2-byte elements:
+    the split-K kernel holds one row in a wave's 16-byte lanes)."""
+    return dtype in _HIP_DTYPES and head_dim in _HIP_HEAD_DIMS and not (head_dim == 512 and dtype == torch.float32)
 _checked: dict[tuple, bool] = {}
 
 
@@ -227,7 +233,7 @@ class Attention(nn.Module):
             return False, None
         if tap_active(self.tap_pattern):
             return False, None
-        if q.dtype not in _HIP_DTYPES or self.hd not in _HIP_HEAD_DIMS:
+        if not hip_shape_ok(q.dtype, self.hd):
             return False, None
         if cache is not None and cache.k[self.layer_idx].dtype != q.dtype:
             return False, None   # the reference's SDPA needs q and the cache in one dtype too

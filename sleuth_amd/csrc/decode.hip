@@ -1451,8 +1451,12 @@ void verify_mfma_persistent_kernel(SplitParams p) {
 // ---------------------------------------------------------------- host side
 static int vec_of(int dtype) { return dtype == FORGE_F32 ? 4 : 8; }
 
-static int rows_per_block(int rows_total) {
-  if (rows_total >= 8) return 8;
+// Query rows per split-K block: up to 8, and up to 4 at head dim 512, where the block's
+// merge buffer (4 waves x rows x D fp32) would otherwise exceed the 64 KB of static LDS.
+template <int D> constexpr int split_max_rows() { return D >= 512 ? 4 : 8; }
+static int rows_per_block(int rows_total, int D) {
+  const int cap = D >= 512 ? split_max_rows<512>() : split_max_rows<256>();
+  if (rows_total >= cap) return cap;
   int r = 1;
   while (r < rows_total) r <<= 1;
   return r;
@@ -1460,7 +1464,12 @@ static int rows_per_block(int rows_total) {
 
 static int keys_per_iter(int dtype, int D) { return (kSplitThreads / (D / vec_of(dtype))) * kSplitNK; }
 
-static bool head_dim_ok(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
+// Head dims of the split-K kernel: a key row is held by D / (16 bytes) lanes, at most a
+// wave, so 512 needs 2-byte elements (bf16/fp16: the full-attention layers of Gemma 4,
+// reference kv_cache.py:12-13).
+static bool head_dim_ok(int dtype, int D) {
+  return D == 32 || D == 64 || D == 128 || D == 256 || (D == 512 && dtype != FORGE_F32);
+}
 
 // The MFMA path (verify_mfma_kernel) serves bf16/fp16 head dim 128/256 with G >= 4 query
 // heads per KV head, whatever T is (so verify and decode of one model share it).
@@ -1537,7 +1546,7 @@ static int auto_chunk(int dtype, int B, int /*T*/, int H, int K, int D, int64_t 
     const int cap = B <= kVerifyPersistRows ? kMaxVerifyChunkPersist : kMaxVerifyChunk;
     return chunk < cap ? chunk : cap;
   }
-  const int rows = rows_per_block(G * T);
+  const int rows = rows_per_block(G * T, D);
   const int64_t n_rb = (G * T + rows - 1) / rows;
   const int64_t pairs = (int64_t)B * K * n_rb;
   // At least 4 block iterations per unit (a one-iteration unit spends most of its time in
@@ -1574,7 +1583,7 @@ static int uniform_chunk(int dtype, int B, int H, int K, int D, int64_t max_kv_l
     const bool split = pairs * 4 <= (int64_t)verify_blocks_per_cu(D) * device_cus();
     return split && chunk > kMaxVerifyChunk ? kMaxVerifyChunk : chunk;
   }
-  const int rows = rows_per_block(G);
+  const int rows = rows_per_block(G, D);
   const int64_t pairs = (int64_t)B * K * ((G + rows - 1) / rows);
   const int kpi = keys_per_iter(dtype, D);
   const int64_t min_chunk = 4 * (int64_t)kpi;  // at least 4 block iterations per unit
@@ -1645,7 +1654,12 @@ static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
     case 1: kern = reinterpret_cast<const void*>(&splitk_kernel<T, D, 1>); break;
     case 2: kern = reinterpret_cast<const void*>(&splitk_kernel<T, D, 2>); break;
     case 4: kern = reinterpret_cast<const void*>(&splitk_kernel<T, D, 4>); break;
-    case 8: kern = reinterpret_cast<const void*>(&splitk_kernel<T, D, 8>); break;
+    case 8:
+      if constexpr (split_max_rows<D>() >= 8) {
+        kern = reinterpret_cast<const void*>(&splitk_kernel<T, D, 8>);
+        break;
+      }
+      return set_error("internal: rows per block");
     default: return set_error("internal: rows per block");
   }
   dim3 grid;
@@ -1677,8 +1691,12 @@ static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
   switch (rows) {
 #define FORGE_ROWS(R) \
   case R: hipLaunchKernelGGL((splitk_kernel<T, D, R>), grid, dim3(kSplitThreads), 0, s, p); break;
-    FORGE_ROWS(1) FORGE_ROWS(2) FORGE_ROWS(4) FORGE_ROWS(8)
+    FORGE_ROWS(1) FORGE_ROWS(2) FORGE_ROWS(4)
 #undef FORGE_ROWS
+    case 8:
+      if constexpr (split_max_rows<D>() >= 8)
+        hipLaunchKernelGGL((splitk_kernel<T, D, 8>), grid, dim3(kSplitThreads), 0, s, p);
+      break;
   }
   int st = check_launch();
   if (st || p.max_chunks < 2) return st;
@@ -1746,7 +1764,10 @@ static int launch_split(const SplitParams& p, int D, int rows, hipStream_t s) {
     case 64: return launch_split_d<T, 64>(p, rows, s);
     case 128: return launch_split_d<T, 128>(p, rows, s);
     case 256: return launch_split_d<T, 256>(p, rows, s);
-    default: return set_error("forge_attn_decode: head dim must be 32, 64, 128 or 256");
+    case 512:
+      if constexpr (sizeof(T) == 2) return launch_split_d<T, 512>(p, rows, s);
+      return set_error("forge_attn_decode: head dim 512 needs bf16 or fp16");
+    default: return set_error("forge_attn_decode: head dim must be 32, 64, 128 or 256 (or 512 in bf16/fp16)");
   }
 }
 
@@ -1756,13 +1777,13 @@ using namespace forge;
 
 extern "C" int forge_attn_decode_chunk(int dtype, int B, int T, int H, int K, int D,
                                        int64_t max_kv_len) {
-  if (K <= 0 || H % K || !head_dim_ok(D) || T <= 0) return 0;
+  if (K <= 0 || H % K || !head_dim_ok(dtype, D) || T <= 0) return 0;
   return auto_chunk(dtype, B, T, H, K, D, max_kv_len);
 }
 
 extern "C" int forge_attn_decode_chunk_uniform(int dtype, int B, int T, int H, int K, int D,
                                                int64_t max_kv_len) {
-  if (K <= 0 || H % K || !head_dim_ok(D) || T <= 0 || B <= 0) return 0;
+  if (K <= 0 || H % K || !head_dim_ok(dtype, D) || T <= 0 || B <= 0) return 0;
   return uniform_chunk(dtype, B, H, K, D, max_kv_len);
 }
 
@@ -1797,7 +1818,8 @@ int decode_setup(SplitParams& p, int dtype, int B, int T, int H, int K, int D, c
     return set_error("unknown dtype code");
   if (B <= 0 || T <= 0 || H <= 0 || K <= 0) return set_error("sizes must be positive");
   if (H % K) return set_error("n_heads must be a multiple of the KV heads");
-  if (!head_dim_ok(D)) return set_error("forge_attn_decode: head dim must be 32, 64, 128 or 256");
+  if (!head_dim_ok(dtype, D))
+    return set_error("forge_attn_decode: head dim must be 32, 64, 128 or 256 (or 512 in bf16/fp16)");
   if (!q || !k_cache || !v_cache || !out) return set_error("null tensor pointer");
   if ((flags & FORGE_ROPE) && (!cos || !sin)) return set_error("FORGE_ROPE needs cos and sin");
   if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16)
@@ -1884,7 +1906,7 @@ void decode_bind(SplitParams& p, int D, void* ws) {
 int decode_launch(const SplitParams& p, int dtype, int D, hipStream_t s) {
   if (use_verify_mfma(dtype, D, p.G))
     return dtype == FORGE_BF16 ? launch_verify<bf16>(p, D, s) : launch_verify<f16>(p, D, s);
-  const int rows = rows_per_block(p.rows_total);
+  const int rows = rows_per_block(p.rows_total, D);
   switch (dtype) {
     case FORGE_F32: return launch_split<float>(p, D, rows, s);
     case FORGE_BF16: return launch_split<bf16>(p, D, rows, s);
@@ -1944,7 +1966,7 @@ extern "C" int forge_attn_decode_append(
   const int groups = kSplitThreads / (D / vec);
   const bool one_block = use_verify_mfma(dtype, D, p.G)
                              ? p.rows_total <= kVerifyRows
-                             : T <= kNewPerLane * groups && rows_per_block(p.rows_total) >= p.rows_total;
+                             : T <= kNewPerLane * groups && rows_per_block(p.rows_total, D) >= p.rows_total;
   const bool fused = one_block &&
                      ((uintptr_t)k | (uintptr_t)v | (uintptr_t)k_weight | (uintptr_t)cos | (uintptr_t)sin) % 16 == 0 &&
                      (sknb | sknh | sknt | svnb | svnh | svnt) % vec == 0;

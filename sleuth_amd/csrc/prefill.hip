@@ -503,13 +503,323 @@ static int launch_prefill_d(PrefillParams p, hipStream_t s) {
   return check_launch();
 }
 
+// ---------------------------------------------------------------- head dim 512
+// Head dim 512 (Gemma 4's full-attention layers: 1 KV head of 512, reference
+// kv_cache.py:12-13). A wave's 32 queries would need 128 registers of Q^T and 256 of output
+// accumulators, so here the head dim is split over the block instead: a block of 4 waves
+// owns 32 queries of one (b, head), and wave w holds channels 128w .. 128w + 127 of Q^T and
+// of the output. Per key tile (32 keys, two LDS stages of 32 KB K + 32 KB V):
+//   * each wave computes the partial scores of its channels, S_w^T = K[:, slice] . Q^T[slice]
+//     (8 MFMAs), and stores them in LDS; after a barrier every wave adds the four partials
+//     in the same order (waves 0..3), so all waves hold identical scores;
+//   * every wave runs the same online softmax (the running max and sum are identical in
+//     all waves) and accumulates its own 128 output channels, O^T += V^T[slice] . P^T
+//     (8 MFMAs).
+// The q RMSNorm sums the squares of the four slices through LDS in the same order; RoPE
+// pairs channel c with c ^ 256, so each lane also loads its channels' partners.
+struct WideTile {
+  static constexpr int D = 512;
+  static constexpr int WAVES = 4;
+  static constexpr int BM = 32;                          // queries per block
+  static constexpr int BN = 32;                          // keys per tile
+  static constexpr int NCH = D / 8;
+  static constexpr int ROWB = 2 * D;
+  static constexpr int TILEB = BN * ROWB;                // 32 KB
+  static constexpr int LOADS = TILEB / (WAVES * 1024);   // 8
+  static constexpr int STAGES = 2;
+  static constexpr int PART_BYTES = WAVES * 64 * 16 * 4; // the waves' partial scores
+  static constexpr int SS_BYTES = WAVES * 32 * 4;        // the q slices' sums of squares
+  static constexpr int LDS_BYTES = STAGES * 2 * TILEB + PART_BYTES + SS_BYTES;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+void prefill_wide_kernel(PrefillParams p) {
+  using V8 = typename Mfma<T>::vec;
+  using TL = WideTile;
+  constexpr int D = TL::D;
+  constexpr int BN = TL::BN;
+  constexpr int KSTEPS = 8;    // 16-channel MFMA k-steps over a wave's 128 channels
+  constexpr int DB = 4;        // 32-channel output blocks per wave
+  constexpr int HALVES = BN / 16;
+
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  float* part = reinterpret_cast<float*>(smem + TL::STAGES * 2 * TL::TILEB);   // [wave][lane][16]
+  float* sh_ss = part + TL::WAVES * 64 * 16;                                     // [wave][32]
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lane = tid % kWave;
+  const int n = lane & 31;
+  const int hi = lane >> 5;
+
+  // block -> (query tile, head, batch), heavy (late) causal tiles first
+  const int HB = p.H * p.B;
+  const int qt = p.nqt - 1 - (int)blockIdx.x / HB;
+  const int hb = (int)blockIdx.x % HB;
+  const int b = hb % p.B, h = hb / p.B;
+  const int kvh = h / p.G;
+
+  const int i_q = qt * TL::BM + n;
+  const bool valid_q = i_q < p.T;
+  const int64_t S = p.offset + p.T;
+  const int64_t q_first = p.offset + (int64_t)qt * TL::BM;
+  const int q_last_idx = qt * TL::BM + TL::BM - 1 < p.T - 1 ? qt * TL::BM + TL::BM - 1 : p.T - 1;
+  const int64_t blk_kmax = p.offset + q_last_idx;
+  int64_t blk_kmin = p.window > 0 ? q_first - p.window + 1 : 0;
+  if (blk_kmin < 0) blk_kmin = 0;
+  const int32_t* dl = p.doc_lo ? p.doc_lo + b * p.sdb : nullptr;
+  int d_lane = 0, d_first = 0, d_last = 0;
+  if (dl) {
+    d_lane = dl[i_q < p.T ? i_q : p.T - 1];
+    d_first = __builtin_amdgcn_readfirstlane(d_lane);
+    d_last = __builtin_amdgcn_readlane(d_lane, q_last_idx - qt * TL::BM);
+    if (d_first > blk_kmin) blk_kmin = d_first;
+  }
+  const int kt_begin = (int)(blk_kmin / BN);
+  const int kt_end = (int)(blk_kmax / BN);
+
+  const char* kgb = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + b * p.skb + kvh * p.skh);
+  const char* vgb = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + b * p.skb + kvh * p.skh);
+  auto issue = [&](int kt, int stage) {
+    const int64_t key0 = (int64_t)kt * BN;
+    const char* kt_base = kgb + key0 * p.sks * 2;
+    const char* vt_base = vgb + key0 * p.sks * 2;
+    const unsigned kdst = lds_offset(smem + (2 * stage) * TL::TILEB + wave * TL::LOADS * 1024);
+#pragma unroll
+    for (int i = 0; i < TL::LOADS; ++i) {
+      const int slot = (wave * TL::LOADS + i) * 64 + lane;
+      const int row = slot / TL::NCH, pch = slot % TL::NCH;
+      const int64_t key = key0 + row < S ? key0 + row : S - 1;   // rows past the end are masked
+      const unsigned rb = (unsigned)((key - key0) * p.sks * 2);
+      lds_dma16(kt_base, rb + (pch ^ swz_k<D>(row)) * 16, kdst + i * 1024);
+      lds_dma16(vt_base, rb + (pch ^ swz_v<D>(row)) * 16, kdst + TL::TILEB + i * 1024);
+    }
+  };
+  issue(kt_begin, 0);
+
+  // ---- Q^T slice: channels 128 wave + 16 s + 8 hi + e, RMSNorm over all 512 channels
+  // (slice sums added through LDS in wave order), RoPE with the partner c ^ 256.
+  V8 qreg[KSTEPS];
+  {
+    const int c0 = 128 * wave + 8 * hi;
+    const int pc0 = 128 * (wave ^ 2) + 8 * hi;   // partner channels
+    float x[KSTEPS][8], z[KSTEPS][8];
+    const T* src = static_cast<const T*>(p.q) + b * p.sqb + h * p.sqh + (int64_t)(valid_q ? i_q : 0) * p.sqt;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      unpack16<T>(load16(src + c0 + 16 * s), x[s]);
+      unpack16<T>(load16(src + pc0 + 16 * s), z[s]);
+    }
+    if (p.flags & FORGE_NORM_QK) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += x[s][e] * x[s][e];
+      ss += __shfl_xor(ss, 32, kWave);
+      if (hi == 0) sh_ss[wave * 32 + n] = ss;
+      __syncthreads();
+      const float tot = ((sh_ss[n] + sh_ss[32 + n]) + sh_ss[64 + n]) + sh_ss[96 + n];
+      const float rs = rsqrtf(tot / (float)D + p.eps);
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        float wx[8], wz[8];
+        if (p.qw) {
+          load_f32x8(p.qw + c0 + 16 * s, wx);
+          load_f32x8(p.qw + pc0 + 16 * s, wz);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          x[s][e] *= rs;
+          z[s][e] *= rs;
+          if (p.qw) {
+            x[s][e] *= wx[e];
+            z[s][e] *= wz[e];
+          }
+        }
+      }
+    }
+    if ((p.flags & FORGE_ROPE) && valid_q) {
+      const float* cr = p.cos + (int64_t)i_q * p.cst;
+      const float* sr = p.sin + (int64_t)i_q * p.cst;
+      const bool first_half = wave < 2;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        float cv[8], sv[8];
+        load_f32x8(cr + c0 + 16 * s, cv);
+        load_f32x8(sr + c0 + 16 * s, sv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          x[s][e] = first_half ? x[s][e] * cv[e] - z[s][e] * sv[e] : x[s][e] * cv[e] + z[s][e] * sv[e];
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qreg[s][e] = from_f32<T>(valid_q ? x[s][e] : 0.0f);
+  }
+
+  const int off = (int)p.offset;
+  const int S32 = (int)S;
+  const int qpos32 = (int)(p.offset + i_q);
+  const int wq_lo = off + qt * TL::BM, wq_hi = off + q_last_idx;
+  const int k_rd = n * TL::ROWB;
+  const int k_sw = swz_k<D>(n);
+  const int g = lane >> 4, kq = (lane >> 2) & 3, qq = lane & 3;
+  const int v_row = 4 * (g >> 1) + kq;
+  const int v_sw = swz_v<D>(v_row);
+  const int v_chlo = 2 * (g & 1) + (qq >> 1);
+  const int v_byte = 8 * (qq & 1);
+
+  floatx16 oacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int x = 0; x < 16; ++x) oacc[d][x] = 0.0f;
+  float m_run = kNegInf, l_run = 0.0f;
+  const float c = p.scale_log2;
+
+  for (int kt = kt_begin; kt <= kt_end; ++kt) {
+    const int stage = (kt - kt_begin) & 1;
+    wait_vm<0>();
+    __syncthreads();   // tile kt in LDS; every wave is done with tile kt - 1 and its partials
+    if (kt + 1 <= kt_end) issue(kt + 1, stage ^ 1);
+    const char* kl = smem + (2 * stage) * TL::TILEB + k_rd;
+    const char* vl = smem + (2 * stage + 1) * TL::TILEB;
+
+    // partial scores of this wave's channels
+    floatx16 sp;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) sp[x] = 0.0f;
+#pragma unroll
+    for (int st = 0; st < KSTEPS; ++st) {
+      const V8 a = *reinterpret_cast<const V8*>(kl + ((16 * wave + ((2 * st + hi) ^ k_sw)) << 4));
+      sp = Mfma<T>::run(a, qreg[st], sp);
+    }
+    {
+      float4* dst = reinterpret_cast<float4*>(part + (wave * 64 + lane) * 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[i] = make_float4(sp[4 * i], sp[4 * i + 1], sp[4 * i + 2], sp[4 * i + 3]);
+    }
+    __syncthreads();
+    floatx16 sacc;
+    {
+      float4 pw[4][4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pw[w][i] = reinterpret_cast<const float4*>(part + (w * 64 + lane) * 16)[i];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sacc[4 * i + 0] = ((pw[0][i].x + pw[1][i].x) + pw[2][i].x) + pw[3][i].x;
+        sacc[4 * i + 1] = ((pw[0][i].y + pw[1][i].y) + pw[2][i].y) + pw[3][i].y;
+        sacc[4 * i + 2] = ((pw[0][i].z + pw[1][i].z) + pw[2][i].z) + pw[3][i].z;
+        sacc[4 * i + 3] = ((pw[0][i].w + pw[1][i].w) + pw[2][i].w) + pw[3][i].w;
+      }
+    }
+
+    const int key0 = kt * BN;
+    const bool full = key0 + BN - 1 <= wq_lo && key0 + BN - 1 < S32 &&
+                      (p.window <= 0 || wq_hi - key0 < p.window) && q_last_idx - qt * TL::BM == TL::BM - 1 &&
+                      key0 >= d_last;
+    if (!full) {
+      const int base = key0 + 4 * hi;
+      const int top = (qpos32 < S32 - 1 ? qpos32 : S32 - 1) - base;
+      const int lim_hi = valid_q ? top : -1;
+      int lim_lo = p.window > 0 ? qpos32 - p.window + 1 - base : -(1 << 30);
+      if (dl && d_lane - base > lim_lo) lim_lo = d_lane - base;
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        const int ce = 8 * (x >> 2) + (x & 3);
+        sacc[x] = (ce <= lim_hi && ce >= lim_lo) ? sacc[x] : kNegInf;
+      }
+    }
+    float mx = sacc[0];
+#pragma unroll
+    for (int x = 1; x < 16; ++x) mx = fmaxf(mx, sacc[x]);
+    mx = max_xor32(mx);
+    const float mxc = mx * c;
+    if (mxc > m_run + kLazyLog2) {
+      const float alpha = m_run == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(m_run - mxc);
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) oacc[d][x] *= alpha;
+      m_run = mxc;
+    }
+    const float neg_m = m_run == kNegInf ? 0.0f : -m_run;
+    float rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[x], c, neg_m));
+      sacc[x] = pv;
+      rs[x & 3] += pv;
+    }
+    l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
+
+    // O^T += V^T . P^T over this wave's 128 channels
+#pragma unroll
+    for (int hf = 0; hf < HALVES; ++hf) {
+      V8 pb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pb[e] = from_f32<T>(sacc[8 * hf + e]);
+      const char* vrow0 = vl + (16 * hf + v_row) * TL::ROWB + v_byte;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const int ch = (16 * wave + ((4 * d + v_chlo) ^ v_sw)) << 4;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)(vrow0 + ch));
+        const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)(vrow0 + 8 * TL::ROWB + ch));
+        typedef short i16x8 __attribute__((ext_vector_type(8)));
+        const i16x8 av = __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[d] = Mfma<T>::run(__builtin_bit_cast(V8, av), pb, oacc[d]);
+      }
+    }
+  }
+
+  l_run += __shfl_xor(l_run, 32, kWave);
+  if (!valid_q) return;
+  const float inv_l = 1.0f / l_run;
+  T* dst = static_cast<T*>(p.out) + b * p.sob + (int64_t)i_q * p.sot + h * p.soh + 128 * wave;
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      T vals[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vals[j] = from_f32<T>(oacc[d][4 * i + j] * inv_l);
+      *reinterpret_cast<uint2*>(dst + d * 32 + 8 * i + 4 * hi) = *reinterpret_cast<uint2*>(vals);
+    }
+}
+
+template <typename T>
+static int launch_prefill_wide(PrefillParams p, hipStream_t s) {
+  using TL = WideTile;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_wide_kernel<T>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, TL::LDS_BYTES) != hipSuccess)
+      return set_error("forge_attn_prefill: cannot reserve the LDS the kernel needs");
+    attr_set = true;
+  }
+  p.nqt = (p.T + TL::BM - 1) / TL::BM;
+  if ((int64_t)p.nqt * p.H * p.B > 0x7fffffff) return set_error("grid too large");
+  const dim3 grid((unsigned)((int64_t)p.nqt * p.H * p.B));
+  hipLaunchKernelGGL((prefill_wide_kernel<T>), grid, dim3(TL::WAVES * 64), TL::LDS_BYTES, s, p);
+  return check_launch();
+}
+
 template <typename T>
 static int launch_prefill(const PrefillParams& p, int D, hipStream_t s) {
   switch (D) {
     case 64: return launch_prefill_d<T, 64>(p, s);
     case 128: return launch_prefill_d<T, 128>(p, s);
     case 256: return launch_prefill_d<T, 256>(p, s);
-    default: return set_error("forge_attn_prefill: head dim must be 64, 128 or 256");
+    case 512: return launch_prefill_wide<T>(p, s);
+    default: return set_error("forge_attn_prefill: head dim must be 64, 128, 256 or 512");
   }
 }
 
@@ -525,8 +835,8 @@ static int prefill_call(int dtype, int B, int T, int H, int K, int D, const void
                         const int32_t* doc_lo, int64_t sdb, void* stream) {
   if (dtype != FORGE_BF16 && dtype != FORGE_F16)
     return set_error("forge_attn_prefill: dtype must be bf16 or fp16 (use forge_attn_decode)");
-  if (D != 64 && D != 128 && D != 256)
-    return set_error("forge_attn_prefill: head dim must be 64, 128 or 256");
+  if (D != 64 && D != 128 && D != 256 && D != 512)
+    return set_error("forge_attn_prefill: head dim must be 64, 128, 256 or 512");
   if (B <= 0 || T <= 0 || H <= 0 || K <= 0) return set_error("sizes must be positive");
   if (H % K) return set_error("n_heads must be a multiple of the KV heads");
   if (offset < 0) return set_error("offset must be >= 0");

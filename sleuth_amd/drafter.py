@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from .attention import _HIP_DTYPES, _HIP_HEAD_DIMS, _hip_ready, hip_disabled
+from .attention import _hip_ready, hip_shape_ok, hip_disabled
 from .norm import RMSNorm
 from .rope import apply_rope
 
@@ -44,7 +44,7 @@ class DrafterAttention(nn.Module):
     def _use_hip(self, q: torch.Tensor, k: torch.Tensor) -> bool:
         if not q.is_cuda or hip_disabled() or (torch.is_grad_enabled() and q.requires_grad):
             return False
-        if q.dtype not in _HIP_DTYPES or self.hd not in _HIP_HEAD_DIMS or k.dtype != q.dtype:
+        if not hip_shape_ok(q.dtype, self.hd) or k.dtype != q.dtype:
             return False
         _hip_ready(q.device, q.dtype)
         return True

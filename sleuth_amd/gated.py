@@ -19,7 +19,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from .attention import DECODE_MAX_T, _HIP_DTYPES, _HIP_HEAD_DIMS, _hip_ready, hip_disabled
+from .attention import DECODE_MAX_T, _hip_ready, hip_shape_ok, hip_disabled
 from .norm import RMSNorm
 from .rope import apply_rope
 
@@ -35,7 +35,7 @@ class GatedAttention(nn.Module):
     def _use_hip(self, q: torch.Tensor, cache) -> bool:
         if not q.is_cuda or hip_disabled() or (torch.is_grad_enabled() and q.requires_grad):
             return False
-        if q.dtype not in _HIP_DTYPES or self.cfg.head_dim not in _HIP_HEAD_DIMS:
+        if not hip_shape_ok(q.dtype, self.cfg.head_dim):
             return False
         if cache is not None and (getattr(cache, "static", False) or getattr(cache, "ragged", False)):
             return False  # the reference model drives this layer with a plain cache only

@@ -344,7 +344,7 @@ def attn_drafter(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     return attn_decode(q, k_cache, v_cache, scale=scale, pos=int(n_past) - 1, window=w, **kw)
 
 
-PREFILL_HEAD_DIMS = (64, 128, 256)
+PREFILL_HEAD_DIMS = (64, 128, 256, 512)
 
 
 def prefill_supported(q: torch.Tensor) -> bool:
