@@ -904,8 +904,11 @@ template <int D> struct VerifyTile {
   static constexpr int ROWB = 2 * D;
   static constexpr int TILEB = BN * ROWB;
   static constexpr int LOADS = TILEB / (WAVES * 1024);
-  static constexpr int STAGES = 4;              // LDS stages of K and V: three tiles in flight
-  static constexpr int MAX_TOK = ROWS / 4 + 1;  // tokens under one unit's rows (G >= 4)
+  // LDS stages of K and V: three tiles in flight; at head dim 512 (32 KB tiles) two stages
+  // (one tile in flight), the most that fits beside the tables
+  static constexpr int STAGES = D >= 512 ? 2 : 4;
+  static constexpr int MIN_G = D >= 512 ? 8 : 4;          // query heads per KV head the path takes
+  static constexpr int MAX_TOK = ROWS / MIN_G + 1;        // tokens under one unit's rows
   // q gains, cos rows and sin rows (fp32), each region padded to whole KB (the DMA unit)
   static constexpr int TAB_G = (4 * D + 1023) / 1024 * 1024;
   static constexpr int TAB_R = (MAX_TOK * 4 * D + 1023) / 1024 * 1024;
@@ -1117,9 +1120,9 @@ __device__ __forceinline__ void verify_unit(const SplitParams& p, char* smem, co
     for (int i = 0; i < TL::STAGES - 1; ++i) issue(i);
     // this wave's small loads have landed once at most its tile loads remain
     const int pro_tiles = ntiles < TL::STAGES - 1 ? ntiles : TL::STAGES - 1;
-    static_assert(TL::STAGES - 1 == 3, "one wait per prologue tile count");
-    if (pro_tiles >= 3) vwait_vm<6 * TL::LOADS>();
-    else if (pro_tiles == 2) vwait_vm<4 * TL::LOADS>();
+    static_assert(TL::STAGES - 1 == 3 || TL::STAGES - 1 == 1, "one wait per prologue tile count");
+    if (TL::STAGES - 1 == 3 && pro_tiles >= 3) vwait_vm<(TL::STAGES - 1 == 3 ? 6 : 2) * TL::LOADS>();
+    else if (TL::STAGES - 1 == 3 && pro_tiles == 2) vwait_vm<(TL::STAGES - 1 == 3 ? 4 : 2) * TL::LOADS>();
     else vwait_vm<2 * TL::LOADS>();
     __syncthreads();  // every wave's q rows and tables are in LDS (tiles may be in flight)
     const T* qrow = qraw + qr * D + qx;
@@ -1366,8 +1369,12 @@ __device__ __forceinline__ void verify_unit(const SplitParams& p, char* smem, co
 constexpr int kVerifyPersistRows = 512;
 
 // MFMA verify kernel, dense grid: one block per (chunk, KV head x row block, batch row).
+// Waves per SIMD: two blocks per CU at head dims 128/256; at 512 one (its LDS, and the Q^T
+// operands of 32 rows, 128 registers).
+template <int D> constexpr int verify_waves_per_eu() { return D >= 512 ? 1 : 2; }
+
 template <typename T, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(verify_waves_per_eu<D>())))
 void verify_mfma_kernel(SplitParams p) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   const int b = blockIdx.z;
@@ -1381,7 +1388,7 @@ void verify_mfma_kernel(SplitParams p) {
 // end and the blocks that stream faster take more units. (A kernel of its own: with both
 // grids in one, the dense grid's registers grew from 150 to 212 at head dim 128.)
 template <typename T, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(verify_waves_per_eu<D>())))
 void verify_mfma_persistent_kernel(SplitParams p) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   __shared__ int sh_pref[kVerifyPersistRows + 1];
@@ -1475,13 +1482,15 @@ static bool head_dim_ok(int dtype, int D) {
 // heads per KV head, whatever T is (so verify and decode of one model share it).
 // Blocks of the MFMA verify kernel one CU holds (its LDS, 160 KB per CU, is the limit).
 static int verify_blocks_per_cu(int D) {
-  const int lds = D == 256 ? VerifyTile<256>::LDS_BYTES : VerifyTile<128>::LDS_BYTES;
+  const int lds = D == 512 ? VerifyTile<512>::LDS_BYTES
+                           : D == 256 ? VerifyTile<256>::LDS_BYTES : VerifyTile<128>::LDS_BYTES;
   const int n = (160 * 1024) / lds;
   return n < 1 ? 1 : (n > 2 ? 2 : n);
 }
 
 static bool use_verify_mfma(int dtype, int D, int G) {
-  return dtype != FORGE_F32 && (D == 128 || D == 256) && G >= 4;
+  return dtype != FORGE_F32 && (((D == 128 || D == 256) && G >= VerifyTile<128>::MIN_G) ||
+                                (D == 512 && G >= VerifyTile<512>::MIN_G));
 }
 constexpr int kVerifyRows = 32;
 
@@ -1517,9 +1526,10 @@ static int verify_round_chunk(int B, int H, int K, int D, int64_t max_kv_len) {
   chunk = (chunk + 31) / 32 * 32;
   // At least as many tiles as the pipeline keeps in flight: a shorter unit cannot use its
   // prefetch and is mostly prologue (C5 window 1024: 64-key chunks 23.2 us, 96-key 20.9 us).
+  // (At head dim 512, with one tile in flight, the same three-tile minimum.)
   constexpr int kMinTiles = VerifyTile<128>::STAGES - 1;
-  static_assert(VerifyTile<128>::STAGES == VerifyTile<256>::STAGES &&
-                VerifyTile<128>::BN == VerifyTile<256>::BN, "one tile shape for both head dims");
+  static_assert(VerifyTile<128>::STAGES == VerifyTile<256>::STAGES && VerifyTile<128>::BN == VerifyTile<256>::BN &&
+                VerifyTile<128>::BN == VerifyTile<512>::BN, "one tile shape for every head dim");
   const int64_t min_chunk = (int64_t)kMinTiles * VerifyTile<128>::BN;
   return (int)(chunk < min_chunk ? min_chunk : chunk);
 }
@@ -1754,7 +1764,8 @@ static int launch_verify_d(SplitParams p, hipStream_t s) {
 
 template <typename T>
 static int launch_verify(const SplitParams& p, int D, hipStream_t s) {
-  return D == 128 ? launch_verify_d<T, 128>(p, s) : launch_verify_d<T, 256>(p, s);
+  return D == 128 ? launch_verify_d<T, 128>(p, s)
+                  : D == 256 ? launch_verify_d<T, 256>(p, s) : launch_verify_d<T, 512>(p, s);
 }
 
 template <typename T>

@@ -2,7 +2,8 @@
 sleuth/forge/infer/kv_cache.py:12-13), values taken from the keys before their norm and RoPE
 (v_from_k, attention.py:108), values RMS-normalised without a gain (v_norm, 115-116) and
 attention scale 1.0 (attn_scale, 84). Head dim 512 runs on forge_attn_prefill's
-head-dim-split MFMA kernel and on the split-K kernel (bf16/fp16).
+head-dim-split MFMA kernel, on the MFMA verify/decode kernel with 8 or more query heads per
+KV head, and on the split-K kernel below that (bf16/fp16).
 
 Against the oracle on the same seeded inputs (bf16/fp16 max-abs <= 2e-2): prefill with
 offsets, windows and documents; ragged decode and a 4-token verify; the fused cache write
@@ -111,7 +112,7 @@ def _decode_case(seed, dtype, H, K, T, lens, chunk=0):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("H,K", [(16, 1), (8, 2), (4, 1), (1, 1)])
+@pytest.mark.parametrize("H,K", [(16, 1), (8, 1), (32, 2), (8, 2), (4, 1), (1, 1)])
 @pytest.mark.parametrize("T", [1, 4])
 def test_decode_and_verify_head_dim_512(dtype, H, K, T):
     got, ref = _decode_case(H * 10 + K + T, dtype, H, K, T, [37, 700, 2049, 1500])
@@ -120,10 +121,26 @@ def test_decode_and_verify_head_dim_512(dtype, H, K, T):
     assert err <= tol(dtype)
 
 
-def test_decode_head_dim_512_many_chunks():
-    """A 5000-key row split into 40 chunks of 128 keys (the combine kernel at head dim 512)."""
-    got, ref = _decode_case(5, torch.bfloat16, 16, 1, 1, [5000, 130], chunk=128)
+@pytest.mark.parametrize("H", [16, 4])
+def test_decode_head_dim_512_many_chunks(H):
+    """A 5000-key row split into 40 chunks of 128 keys (the combine kernel at head dim 512),
+    on the MFMA path (16 q heads per KV head) and the split-K kernel (4)."""
+    got, ref = _decode_case(5, torch.bfloat16, H, 1, 1, [5000, 130], chunk=128)
     assert max_abs(got, ref) <= 2e-2
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_decode_head_dim_512_host_position(T):
+    """One position for every row (the dense grid with the uniform chunk rule), 16 q heads
+    per KV head, against the oracle."""
+    g = gen(21 + T)
+    B, H, K, L = 4, 16, 1, 3000
+    kc = (0.2 * randn(g, B, K, L + 5, D)).to(torch.bfloat16)
+    vc = randn(g, B, K, L + 5, D, dtype=torch.bfloat16)
+    q = randn(g, B, T, H, D, dtype=torch.bfloat16).transpose(1, 2)
+    ref = oracle.ragged_decode(q.float(), kc.float(), vc.float(), [L] * B, 0, SCALE)
+    got = ops().attn_decode(q.to(DEV), kc.to(DEV), vc.to(DEV), scale=SCALE, pos=L - T)
+    assert max_abs(got.cpu(), ref.transpose(1, 2)) <= 2e-2
 
 
 def test_verify_rows_equal_decodes_head_dim_512():
