@@ -506,6 +506,21 @@ def main() -> int:
     err_prefill = check_prefill(pf)
     print(f"[bench] outputs checked against fp32 torch: decode max-abs {err_decode:.2e} (longest and "
           f"shortest rows), prefill max-abs {err_prefill:.2e}", file=sys.stderr, flush=True)
+    p_flops, p_flops_full = pf.flops(), pf.flops_full_s()
+    del pf
+    torch.cuda.empty_cache()
+    # Gemma 4's full-attention layer shape: 1 x 4096 causal, 16 q / 1 KV head of 512 (reported)
+    pg = PrefillWorkload(1, 4096, 16, 1, 512, 1e6, dt, dev)
+    pg.append()
+    warm(pg.attend)
+    t_g4 = time_loop(pg.attend, max(3, args.steps // 2), max(1, args.warmup // 2))
+    g4_prefill = {"config": "1 x 4096 causal, 16 q / 1 kv heads, head dim 512, bf16, QK-norm, RoPE theta 1e6",
+                  "us": round(t_g4 * 1e6, 2), "TFLOPs": round(pg.flops() / t_g4 / 1e12, 1),
+                  "frac": round(pg.flops() / t_g4 / 1e12 / BF16_PEAK_TFLOPS, 4),
+                  "kernel": "forge::prefill_wide_kernel<bf16>"}
+    print(f"[bench] Gemma-4 full-layer prefill (hd 512): {g4_prefill}", file=sys.stderr, flush=True)
+    del pg
+    torch.cuda.empty_cache()
     gemm = gemm_tflops(dev)
     print(f"[bench] bf16 8192^3 library GEMM {gemm:.0f} TFLOP/s", file=sys.stderr, flush=True)
     sdpa = sdpa_reference(dev)
@@ -543,7 +558,7 @@ def main() -> int:
         # the reference's convention (sleuth/forge/model/flops.py:84-89): 4*H*hd*S FLOPs per
         # token forward with S the full 4096, i.e. twice the causal count above; for
         # comparison only (the roofline fraction uses the causal count)
-        "prefill_tflops_full_s_convention": round(p_tflops * pf.flops_full_s() / pf.flops(), 1),
+        "prefill_tflops_full_s_convention": round(p_tflops * p_flops_full / p_flops, 1),
         "prefill_step_ms": round(t_pstep * 1e3, 4),
         # the whole prefill step (forge_kv_append of the 4 x 4096 keys and values, then the
         # attention kernel) against the same causal FLOP count
@@ -566,9 +581,10 @@ def main() -> int:
         "roofline_prefill": {"bound": "mfma", "kernel": "forge::prefill_kernel<bf16,128>",
                              "achieved": round(p_tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(p_tflops / BF16_PEAK_TFLOPS, 4),
-                             "traffic": read_traffic("prefill_c3_traffic"), "flops": pf.flops(),
+                             "traffic": read_traffic("prefill_c3_traffic"), "flops": p_flops,
                              "library_gemm_tflops": round(gemm, 1),
                              "frac_of_library_gemm": round(p_tflops / gemm, 4)},
+        "prefill_gemma4_full_hd512": g4_prefill,
     }
     if not args.no_cpu:
         print("[bench] CPU baseline (decode sample) ...", file=sys.stderr, flush=True)
@@ -718,6 +734,11 @@ EXTRA_CONFIGS = {
     "C5_verify_b8_T4_8q1kv_hd256_global": dict(lens=[8196] * 8, H=8, K=1, D=256, theta=1e6, T=4, n_layers=12),
     "C5_verify_b8_T4_8q1kv_hd256_window1024": dict(lens=[8196] * 8, H=8, K=1, D=256, theta=1e6, T=4,
                                                    window=1024, n_layers=12),
+    # Gemma 4's full-attention layer shape (1 KV head of 512, kv_cache.py:12-13): decode and a
+    # 4-token verify (not a BASELINE config; reported beside them)
+    "G4full_decode_b16_16q1kv_hd512_S8192": dict(lens=[8192] * 16, H=16, K=1, D=512, theta=1e6, n_layers=2),
+    "G4full_verify_b16_T4_16q1kv_hd512_S8192": dict(lens=[8192] * 16, H=16, K=1, D=512, theta=1e6, T=4,
+                                                    n_layers=2),
 }
 # the rocprofv3 traffic summary of each (profiles/<name>.txt)
 EXTRA_TRAFFIC = {
@@ -725,11 +746,14 @@ EXTRA_TRAFFIC = {
     "C3_decode_b32_16q8kv_hd128_S8192": "decode_c3_traffic",
     "C5_verify_b8_T4_8q1kv_hd256_global": "verify_c5_global_traffic",
     "C5_verify_b8_T4_8q1kv_hd256_window1024": "verify_c5_window1024_traffic",
+    "G4full_decode_b16_16q1kv_hd512_S8192": "decode_g4full_traffic",
+    "G4full_verify_b16_T4_16q1kv_hd512_S8192": "verify_g4full_traffic",
 }
 
 
 def extra_configs(dev, args) -> dict:
-    """Configs C2, C3-decode and C5 (reported; BASELINE sets no target for them). Small
+    """Configs C2, C3-decode and C5, and Gemma 4's full-attention layer shape (reported;
+    BASELINE sets no target for them). Small
     working sets rotate through several layer caches so the ~256 MB MALL does not serve
     them. The roofline uses the attention call replayed from a HIP graph (how decode steps
     run, and without the host's per-call launch cost, which exceeds these calls' GPU time);
