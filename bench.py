@@ -451,7 +451,7 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="skip the reported configs C2, C3-decode, C5")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--config", default="", help="with --only extra: run only the configs whose name contains this")
-    ap.add_argument("--only", choices=["decode", "prefill", "copy", "gemm", "sdpa", "qkv", "extra"],
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill512", "copy", "gemm", "sdpa", "qkv", "extra"],
                     help="time one workload (for rocprofv3 runs); copy = a 1 GiB torch copy, the "
                          "known-size kernel that calibrates the HBM byte counters; gemm = a bf16 "
                          "library GEMM, the practical MFMA rate beside the vendor peak; sdpa = torch's "
@@ -517,7 +517,7 @@ def main() -> int:
     g4_prefill = {"config": "1 x 4096 causal, 16 q / 1 kv heads, head dim 512, bf16, QK-norm, RoPE theta 1e6",
                   "us": round(t_g4 * 1e6, 2), "TFLOPs": round(pg.flops() / t_g4 / 1e12, 1),
                   "frac": round(pg.flops() / t_g4 / 1e12 / BF16_PEAK_TFLOPS, 4),
-                  "kernel": "forge::prefill_wide_kernel<bf16>"}
+                  "kernel": "forge::prefill_wide_kernel<bf16>", "traffic": read_traffic("prefill_g4full_traffic")}
     print(f"[bench] Gemma-4 full-layer prefill (hd 512): {g4_prefill}", file=sys.stderr, flush=True)
     del pg
     torch.cuda.empty_cache()
@@ -709,6 +709,14 @@ def run_only(args, dev) -> int:
         ta = time_loop(pf.attend, args.steps, args.warmup)
         print(json.dumps({"workload": "C3 prefill step", "us": round(t * 1e6, 2), "attention_us": round(ta * 1e6, 2),
                           "attention_tflops": round(pf.flops() / ta / 1e12, 1)}), flush=True)
+    elif args.only == "prefill512":
+        pf = PrefillWorkload(1, 4096, 16, 1, 512, 1e6, torch.bfloat16, dev)
+        pf.append()
+        warm(pf.attend)
+        ta = time_loop(pf.attend, args.steps, args.warmup)
+        print(json.dumps({"workload": "Gemma-4 full-layer prefill, 1 x 4096, 16 q / 1 kv heads, hd 512",
+                          "attention_us": round(ta * 1e6, 2), "attention_tflops": round(pf.flops() / ta / 1e12, 1)}),
+              flush=True)
     elif args.only == "extra":
         print(json.dumps(extra_configs(dev, args)), flush=True)
     elif args.only == "sdpa":
