@@ -954,11 +954,12 @@ template <int N> __device__ __forceinline__ void vwait_vm() {
 // new token sits at position `base`), keys of chunk c_in (absolute; with p.span_chunks,
 // counted from the unit's first visible chunk). The caller passes block-uniform arguments
 // and a converged block; the unit may leave early, block-uniformly, and uses all of the
-// dynamic LDS `smem`.
+// dynamic LDS `smem`. This form (head dim 512) fills the LDS stages with direct loads; head
+// dims 128 and 256 take verify_unit_staged below.
 template <typename T, int D>
-__device__ __forceinline__ void verify_unit(const SplitParams& p, char* smem, const int b,
-                                            const int base, const int kvh, const int rb,
-                                            const int c_in) {
+__device__ __forceinline__ void verify_unit_dma(const SplitParams& p, char* smem, const int b,
+                                                const int base, const int kvh, const int rb,
+                                                const int c_in) {
   using V8 = typename VMfma<T>::vec;
   using TL = VerifyTile<D>;
   constexpr int BN = TL::BN;
@@ -1278,9 +1279,23 @@ __device__ __forceinline__ void verify_unit(const SplitParams& p, char* smem, co
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int x = 0; x < 16; ++x) sc[j][x] = 0.0f;
+    {
+      // K operands of k-step s + 2 read before the MFMA of step s (see verify_unit_staged)
+      auto kread = [&](int st) { return *reinterpret_cast<const V8*>(kl + (((2 * st + hi) ^ k_sw) << 4)); };
+      V8 k0 = kread(0), k1 = kread(1), k2 = k1;
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s)
-      sc[s & 3] = VMfma<T>::run(*reinterpret_cast<const V8*>(kl + (((2 * s + hi) ^ k_sw) << 4)), qreg[s], sc[s & 3]);
+      for (int s = 0; s < KSTEPS; ++s) {
+        if (s + 2 < KSTEPS) {
+          k2 = kread(s + 2);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        sc[s & 3] = VMfma<T>::run(k0, qreg[s], sc[s & 3]);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        k0 = k1;
+        k1 = k2;
+      }
+    }
     v_floatx16 sacc;
 #pragma unroll
     for (int x = 0; x < 16; ++x) sacc[x] = (sc[0][x] + sc[1][x]) + (sc[2][x] + sc[3][x]);
@@ -1363,15 +1378,503 @@ __device__ __forceinline__ void verify_unit(const SplitParams& p, char* smem, co
   }
 }
 
+// Head dims 128 and 256: the K and V tiles go from HBM into registers (16-byte
+// non-temporal loads, two tiles in flight) and the threads write them into two LDS stages
+// with the same swizzled layouts. A CU streams about 23-30 GB/s through direct-to-LDS loads
+// whatever the waves and depth, against 36-48 GB/s through registers (7.3 against 5.9 TB/s
+// over the chip), and the q rows and tables, loaded first into registers, no longer queue
+// behind the tiles. LDS: two stages of K and V, the normalised q rows (chunk-swizzled by row,
+// so the Q^T operand reads are conflict-free) and the tables.
+template <int D> struct StagedTile {
+  static constexpr int WAVES = 4;
+  static constexpr int THREADS = WAVES * 64;
+  static constexpr int ROWS = 32;
+  static constexpr int BN = 32;                                 // keys per tile
+  static constexpr int NCH = D / 8;                             // 16-byte chunks per key row
+  static constexpr int ROWB = 2 * D;
+  static constexpr int TILEB = BN * ROWB;                       // one K (or V) tile
+  static constexpr int PER = TILEB / (THREADS * 16);            // pieces per thread per tile
+  static constexpr int MAX_TOK = ROWS / VerifyTile<D>::MIN_G + 1;
+  static constexpr int TAB_G = (4 * D + 1023) / 1024 * 1024;
+  static constexpr int TAB_R = (MAX_TOK * 4 * D + 1023) / 1024 * 1024;
+  static constexpr int QS_OFF = 4 * TILEB;                      // after [K0 | V0 | K1 | V1]
+  static constexpr int TAB_OFF = QS_OFF + ROWS * ROWB;
+  static constexpr int LDS_BYTES = TAB_OFF + TAB_G + 2 * TAB_R;
+  static constexpr bool Q_REGS = D <= 128;  // Q^T operands in registers; at 256 read per tile
+  static constexpr int NCHAIN = D <= 128 ? 4 : 2;  // score accumulation chains (registers at 256)
+  static constexpr int NR = D <= 128 ? 2 : 3;      // register sets of tiles in flight
+  static constexpr int DW = D / WAVES;
+  static_assert(PER * THREADS * 16 == TILEB, "a tile splits into whole 16-byte pieces per thread");
+  static_assert(NCH >= 16, "the K swizzle spans 16 chunks");
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void verify_unit_staged(const SplitParams& p, char* smem, const int b,
+                                                   const int base, const int kvh, const int rb,
+                                                   const int c_in) {
+  using V8 = typename VMfma<T>::vec;
+  using TL = StagedTile<D>;
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  constexpr int BN = TL::BN;
+  constexpr int KSTEPS = D / 16;
+  constexpr int DBW = TL::DW / 32;  // 32-channel blocks per wave
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lane = tid % kWave;
+  const int n = lane & 31;
+  const int hi = lane >> 5;
+
+  // this lane's row and its visible keys; the unit's key span (union over valid rows)
+  const int flat = rb * TL::ROWS + n;
+  const bool valid = flat < p.rows_total;
+  const int t = valid ? flat / p.G : 0;
+  const int h = kvh * p.G + (valid ? flat % p.G : 0);
+  int kmin = INT_MAX, kmax = -1;
+  if (valid) visible_range32(base + t, p.window, (int)p.max_len, kmin, kmax);
+  int umin, umax, dummy;
+  {
+    const int r_hi = rb * TL::ROWS + TL::ROWS - 1 < p.rows_total - 1 ? rb * TL::ROWS + TL::ROWS - 1 : p.rows_total - 1;
+    visible_range32(base + rb * TL::ROWS / p.G, p.window, (int)p.max_len, umin, dummy);
+    visible_range32(base + r_hi / p.G, p.window, (int)p.max_len, dummy, umax);
+  }
+  const int c = p.span_chunks ? umin / p.chunk + c_in : c_in;  // absolute chunk
+  const int c0 = c * p.chunk;
+  if (c >= p.max_chunks || c0 > umax || c0 + p.chunk - 1 < umin) return;  // block-uniform
+
+  // New positions in this chunk (forge_attn_decode_append): made and written before any
+  // tile load, as in verify_unit_dma.
+  if (p.kn) {
+    int n_lo = base > c0 ? base : c0;
+    int n_hi = base + p.T - 1 < c0 + p.chunk - 1 ? base + p.T - 1 : c0 + p.chunk - 1;
+    if (n_hi > (int)p.max_len - 1) n_hi = (int)p.max_len - 1;
+    if (n_lo <= n_hi) {  // block-uniform
+      constexpr int VEC = 16 / sizeof(T);
+      constexpr int LPR = D / VEC;
+      constexpr int RPP = 256 / LPR;
+      const int li = tid % LPR, rr = tid / LPR;
+      const int64_t slab = b * p.skb + kvh * p.skh;
+      for (int p0 = n_lo; p0 <= n_hi; p0 += RPP) {
+        const int pp = p0 + rr;
+        const int tt = (pp <= n_hi ? pp : n_hi) - base;
+        const T* kr = static_cast<const T*>(p.kn) + b * p.sknb + kvh * p.sknh + tt * p.sknt + li * VEC;
+        const T* vr = static_cast<const T*>(p.vn) + b * p.svnb + kvh * p.svnh + tt * p.svnt + li * VEC;
+        const bool krope = p.kvflags & FORGE_ROPE;
+        const float* cr = krope ? p.cos + b * p.csb + tt * p.cst : nullptr;
+        const float* sr = krope ? p.sin + b * p.csb + tt * p.cst : nullptr;
+        const uint4 nk = new_row_slice<T, D>(load16(kr), p.kvflags & FORGE_NORM_QK, p.kw, p.eps, cr, sr, li);
+        const uint4 nv = new_row_slice<T, D>(load16(vr), p.kvflags & FORGE_NORM_V, nullptr, p.eps,
+                                             nullptr, nullptr, li);
+        if (pp <= n_hi) {
+          store16(static_cast<T*>(p.kcw) + slab + (int64_t)pp * p.sks + li * VEC, nk);
+          store16(static_cast<T*>(p.vcw) + slab + (int64_t)pp * p.sks + li * VEC, nv);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  }
+  int t_first = umin > c0 ? (umin - c0) / BN : 0;
+  int t_last = (umax - c0) / BN;
+  if (t_last > p.chunk / BN - 1) t_last = p.chunk / BN - 1;
+  const int ntiles = t_last - t_first + 1;
+
+  // ---- q rows, q gains and RoPE rows first (registers), then the first two tiles. Loads
+  // retire in issue order, so q is usable after one round trip while the tiles stream.
+  const bool gains = (p.flags & FORGE_NORM_QK) && p.qw;
+  const bool rope = (p.flags & FORGE_ROPE) != 0;
+  const int tok_lo = rb * TL::ROWS / p.G;
+  const int tok_hi = (rb * TL::ROWS + TL::ROWS - 1 < p.rows_total - 1 ? rb * TL::ROWS + TL::ROWS - 1 : p.rows_total - 1) / p.G;
+  const int ntok = tok_hi - tok_lo + 1;  // <= MAX_TOK for G >= MIN_G
+  char* qs_b = smem + TL::QS_OFF;       // normalised q rows [ROWS][D], chunk c of row r at c ^ (r & 15)
+  char* tab_b = smem + TL::TAB_OFF;     // [gains | cos rows | sin rows], regions padded
+  float* tab = reinterpret_cast<float*>(tab_b);
+  const float* tab_cos = reinterpret_cast<const float*>(tab_b + TL::TAB_G);
+  const float* tab_sin = reinterpret_cast<const float*>(tab_b + TL::TAB_G + TL::TAB_R);
+  // q math split over the waves: this lane normalises and rotates row qr = 8 * wave + lane / 8,
+  // first-half channels qx .. qx + QCH - 1 and their RoPE partners qx + D/2
+  constexpr int QCH = D / 16;
+  const int qr = 8 * wave + (lane >> 3);
+  const int qx = QCH * (lane & 7);
+  const int qflat = rb * TL::ROWS + qr;
+  const bool qvalid = qflat < p.rows_total;
+  const int qtok = qvalid ? qflat / p.G : 0;
+  uint4 qa[QCH / 8], qz[QCH / 8];
+  {
+    const int qh = kvh * p.G + (qvalid ? qflat % p.G : 0);
+    const T* src = static_cast<const T*>(p.q) + b * p.sqb + qh * p.sqh + qtok * p.sqt + qx;
+#pragma unroll
+    for (int j = 0; j < QCH / 8; ++j) {
+      qa[j] = load16(src + 8 * j);
+      qz[j] = load16(src + D / 2 + 8 * j);
+    }
+  }
+  // Tables as rows [gains | ntok cos rows | ntok sin rows] (rows present per the flags): with
+  // 16-byte aligned tables (p.vec_tables) thread tid loads 4 floats of row ps * RPP + tid / V4R
+  // per pass, else single floats. (Index math per value, with a division by ntok, cost about
+  // as much as the loads' round trip.)
+  constexpr int V4R = D / 4;                       // 16-byte pieces per table row
+  constexpr int RPP = TL::THREADS / V4R;           // rows per pass
+  constexpr int NPASS = (1 + 2 * TL::MAX_TOK + RPP - 1) / RPP;
+  const int nrow = (gains ? 1 : 0) + (rope ? 2 * ntok : 0);
+  const float* cos0 = rope ? p.cos + b * p.csb + (int64_t)tok_lo * p.cst : nullptr;
+  const float* sin0 = rope ? p.sin + b * p.csb + (int64_t)tok_lo * p.cst : nullptr;
+  // table row r of this call: source row, and its float offset in `tab`
+  auto tab_src = [&](int r) {
+    const int rr = gains ? r : r + 1;  // 0 gains, 1..ntok cos, ntok+1.. sin
+    return rr == 0 ? p.qw : rr <= ntok ? cos0 + (int64_t)(rr - 1) * p.cst : sin0 + (int64_t)(rr - 1 - ntok) * p.cst;
+  };
+  auto tab_dst = [&](int r) {
+    const int rr = gains ? r : r + 1;
+    return rr == 0 ? 0 : rr <= ntok ? TL::TAB_G / 4 + (rr - 1) * D : (TL::TAB_G + TL::TAB_R) / 4 + (rr - 1 - ntok) * D;
+  };
+  float4 tv[NPASS];
+  const int tx = 4 * (tid % V4R);
+  if (p.vec_tables) {
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int r = ps * RPP + tid / V4R;
+      if (r < nrow) tv[ps] = *reinterpret_cast<const float4*>(tab_src(r) + tx);
+    }
+  } else {
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int r = ps * RPP + tid / V4R;
+      if (r < nrow) {
+        const float* src = tab_src(r) + tx;
+        tv[ps] = make_float4(src[0], src[1], src[2], src[3]);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the tile loads
+
+  // piece j of this thread: 16-byte chunk ch of key row `row` of the tile, written to LDS
+  // chunk position ch ^ swizzle(row); rows past the unit's last key re-read that key (masked)
+  const char* kgb = reinterpret_cast<const char*>(static_cast<const T*>(p.kc) + b * p.skb + kvh * p.skh);
+  const char* vgb = reinterpret_cast<const char*>(static_cast<const T*>(p.vc) + b * p.skb + kvh * p.skh);
+  const int rstride = (int)p.sks * 2;
+  // byte offset of piece j within a full tile (32-bit, from a block-uniform tile base)
+  unsigned poff[TL::PER];
+#pragma unroll
+  for (int j = 0; j < TL::PER; ++j) {
+    const int slot = j * TL::THREADS + tid;
+    poff[j] = (unsigned)((slot / TL::NCH) * rstride + (slot % TL::NCH) * 16);
+  }
+  auto load_tile = [&](int i, u4 (&kr)[TL::PER], u4 (&vr)[TL::PER]) {
+    const int key0 = c0 + (t_first + i) * BN;
+    const int rows_left = umax - key0 + 1;  // block-uniform
+    const char* kt = kgb + (int64_t)key0 * rstride;
+    const char* vt = vgb + (int64_t)key0 * rstride;
+    if (rows_left >= BN) {
+#pragma unroll
+      for (int j = 0; j < TL::PER; ++j) {
+        kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(kt + poff[j]));
+        vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(vt + poff[j]));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < TL::PER; ++j) {
+        const int slot = j * TL::THREADS + tid;
+        const int row = slot / TL::NCH, ch = slot % TL::NCH;
+        const unsigned off = (unsigned)((row < rows_left ? row : rows_left - 1) * rstride + ch * 16);
+        kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(kt + off));
+        vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(vt + off));
+      }
+    }
+  };
+  auto store_tile = [&](int stage, const u4 (&kr)[TL::PER], const u4 (&vr)[TL::PER]) {
+    char* kd = smem + (2 * stage) * TL::TILEB;
+    char* vd = kd + TL::TILEB;
+#pragma unroll
+    for (int j = 0; j < TL::PER; ++j) {
+      const int slot = j * TL::THREADS + tid;
+      const int row = slot / TL::NCH, ch = slot % TL::NCH;
+      *reinterpret_cast<u4*>(kd + row * TL::ROWB + ((ch ^ vswz_k(row)) << 4)) = kr[j];
+      *reinterpret_cast<u4*>(vd + row * TL::ROWB + ((ch ^ vswz_v(row)) << 4)) = vr[j];
+    }
+  };
+  // NR register sets: tile i sits in set i % NR until it moves to LDS, so NR tiles are in
+  // flight while one is computed (about 96 KB per CU either way: three sets of one block at
+  // head dim 256, two sets of each of two blocks at 128; fewer bytes in flight leave a CU
+  // below its share of the HBM bandwidth)
+  constexpr int NR = TL::NR;
+  u4 r0k[TL::PER], r0v[TL::PER], r1k[TL::PER], r1v[TL::PER], r2k[NR > 2 ? TL::PER : 1], r2v[NR > 2 ? TL::PER : 1];
+  // The tables (and the q rows, issued before them) are waited for before the first tile is
+  // requested: every block of the launch requests its q rows at once, and tile requests
+  // issued with them would put each block's q behind the whole launch's first tiles (5 us
+  // at C5's global layer against about one round trip alone).
+#pragma unroll
+  for (int ps = 0; ps < NPASS; ++ps) {
+    const int r = ps * RPP + tid / V4R;
+    if (r < nrow) *reinterpret_cast<float4*>(tab + tab_dst(r) + tx) = tv[ps];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  load_tile(0, r0k, r0v);
+  if (ntiles > 1) load_tile(1, r1k, r1v);
+  if constexpr (NR > 2) {
+    if (ntiles > 2) load_tile(2, r2k, r2v);
+  }
+  __syncthreads();  // tables in LDS
+
+  // Fused RMSNorm + RoPE of this lane's q values in fp32, one rounding (as the split kernel's
+  // q prologue), stored as T in the swizzled q rows.
+  {
+    float a[QCH], z[QCH];
+#pragma unroll
+    for (int j = 0; j < QCH / 8; ++j) {
+      unpack16<T>(qa[j], a + 8 * j);
+      unpack16<T>(qz[j], z + 8 * j);
+    }
+    if (!qvalid) {
+#pragma unroll
+      for (int e = 0; e < QCH; ++e) a[e] = z[e] = 0.0f;
+    }
+    float rs = 1.0f;
+    if (p.flags & FORGE_NORM_QK) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int e = 0; e < QCH; ++e) ss += a[e] * a[e] + z[e] * z[e];
+      ss += __shfl_xor(ss, 1, kWave);
+      ss += __shfl_xor(ss, 2, kWave);
+      ss += __shfl_xor(ss, 4, kWave);
+      rs = rsqrtf(ss / (float)D + p.eps);
+    }
+#pragma unroll
+    for (int j = 0; j < QCH / 8; ++j) {
+      const int x = qx + 8 * j;
+      float* aj = a + 8 * j;
+      float* zj = z + 8 * j;
+      if (gains) {
+        float wa[8], wz[8];
+        load_f32x8(tab + x, wa);
+        load_f32x8(tab + x + D / 2, wz);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          aj[e] = aj[e] * rs * wa[e];
+          zj[e] = zj[e] * rs * wz[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          aj[e] *= rs;
+          zj[e] *= rs;
+        }
+      }
+      if (rope && qvalid) {
+        const float* cr = tab_cos + (qtok - tok_lo) * D;
+        const float* sr = tab_sin + (qtok - tok_lo) * D;
+        float c1[8], s1[8], c2[8], s2[8];
+        load_f32x8(cr + x, c1);
+        load_f32x8(sr + x, s1);
+        load_f32x8(cr + x + D / 2, c2);
+        load_f32x8(sr + x + D / 2, s2);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float a0 = aj[e], z0 = zj[e];
+          aj[e] = a0 * c1[e] - z0 * s1[e];
+          zj[e] = z0 * c2[e] + a0 * s2[e];
+        }
+      }
+      const int sw = qr & 15;
+      *reinterpret_cast<uint4*>(qs_b + qr * TL::ROWB + (((x / 8) ^ sw) << 4)) = pack16<T>(aj);
+      *reinterpret_cast<uint4*>(qs_b + qr * TL::ROWB + ((((x + D / 2) / 8) ^ sw) << 4)) = pack16<T>(zj);
+    }
+  }
+  store_tile(0, r0k, r0v);
+  if (ntiles > NR) load_tile(NR, r0k, r0v);
+  __syncthreads();  // q rows and tile 0 in LDS
+
+  // Q^T operand of k-step s: channels 16s + 8hi .. of row n
+  const char* q_rd = qs_b + n * TL::ROWB;
+  const int q_sw = n & 15;
+  auto qop = [&](int s) { return *reinterpret_cast<const V8*>(q_rd + (((2 * s + hi) ^ q_sw) << 4)); };
+  V8 qreg[TL::Q_REGS ? KSTEPS : 1];
+  if constexpr (TL::Q_REGS) {
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) qreg[s] = qop(s);
+  }
+
+  // LDS read offsets within a tile (as verify_unit_dma's)
+  const int k_rd = n * TL::ROWB;
+  const int k_sw = vswz_k(n);
+  const int g = lane >> 4, kq = (lane >> 2) & 3, qq = lane & 3;
+  const int v_row = 4 * (g >> 1) + kq;
+  const int v_sw = vswz_v(v_row);
+  const int v_chlo = 2 * (g & 1) + (qq >> 1);
+  const int v_byte = 8 * (qq & 1);
+
+  v_floatx16 oacc[DBW];
+#pragma unroll
+  for (int d = 0; d < DBW; ++d)
+#pragma unroll
+    for (int x = 0; x < 16; ++x) oacc[d][x] = 0.0f;
+  float m_run = kNegInf, l_run = 0.0f;
+  const float cl2 = p.scale_log2;
+
+  // One tile: compute tile i from stage i % 2, then move tile i + 1 from its registers (nk,
+  // nv: set (i + 1) % NR) into the other stage (free since the last barrier) and reuse those
+  // registers for tile i + 1 + NR.
+  auto step = [&](int i, u4 (&nk)[TL::PER], u4 (&nv)[TL::PER]) {
+    const int stage = i & 1;
+    const int key0 = c0 + (t_first + i) * BN;
+    const char* kl = smem + (2 * stage) * TL::TILEB + k_rd;
+    const char* vl = smem + (2 * stage + 1) * TL::TILEB;
+
+    // S^T = K . Q^T for the 32 keys of the tile: NCHAIN accumulation chains over the k-steps
+    // (a chain of dependent MFMAs issues at half rate), added in a fixed order
+    // The operands of k-step s + 2 are read before the MFMA of step s is issued (three
+    // register sets), so the LDS latency hides under two MFMAs; the scheduling groups pin
+    // that order (left alone, the compiler reads each step's operands just before its MFMA
+    // and waits for them: one LDS round trip per MFMA).
+    v_floatx16 sc[TL::NCHAIN];
+#pragma unroll
+    for (int j = 0; j < TL::NCHAIN; ++j)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) sc[j][x] = 0.0f;
+    {
+      constexpr int RD = TL::Q_REGS ? 1 : 2;  // LDS reads per k-step
+      auto kread = [&](int st) { return *reinterpret_cast<const V8*>(kl + (((2 * st + hi) ^ k_sw) << 4)); };
+      auto qget = [&](int st) { return TL::Q_REGS ? qreg[TL::Q_REGS ? st : 0] : qop(st); };
+      V8 k0 = kread(0), k1 = kread(1), k2 = k1;
+      V8 q0 = qget(0), q1 = qget(1), q2 = q1;
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * RD, 0);
+#pragma unroll
+      for (int st = 0; st < KSTEPS; ++st) {
+        if (st + 2 < KSTEPS) {
+          k2 = kread(st + 2);
+          q2 = qget(st + 2);
+          __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+        }
+        sc[st % TL::NCHAIN] = VMfma<T>::run(k0, q0, sc[st % TL::NCHAIN]);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        k0 = k1;
+        k1 = k2;
+        q0 = q1;
+        q1 = q2;
+      }
+    }
+    v_floatx16 sacc;
+#pragma unroll
+    for (int x = 0; x < 16; ++x)
+      sacc[x] = TL::NCHAIN == 4 ? (sc[0][x] + sc[1][x]) + (sc[2][x] + sc[TL::NCHAIN - 1][x]) : sc[0][x] + sc[1][x];
+
+    // element x of this lane is key key0 + 8(x/4) + 4hi + x%4 of row n
+    const int lo = kmin - key0 - 4 * hi, top = kmax - key0 - 4 * hi;
+    float mx = kNegInf;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int ce = 8 * (x >> 2) + (x & 3);
+      sacc[x] = (ce >= lo && ce <= top) ? sacc[x] * cl2 : kNegInf;
+      mx = fmaxf(mx, sacc[x]);
+    }
+    mx = max_xor32(mx);
+    if (mx > m_run + kRescaleLog2) {  // (m = -inf: first visible key)
+      const float alpha = m_run == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(m_run - mx);
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DBW; ++d)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) oacc[d][x] *= alpha;
+      m_run = mx;
+    }
+    float rs = 0.0f;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const float pv = sacc[x] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(sacc[x] - m_run);
+      sacc[x] = pv;
+      rs += pv;
+    }
+    l_run += rs;
+
+    // O^T += V^T . P^T over this wave's channels (two 16-key MFMA steps)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      V8 pb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pb[e] = from_f32<T>(sacc[8 * hf + e]);
+      const char* vrow0 = vl + (16 * hf + v_row) * TL::ROWB + v_byte;
+#pragma unroll
+      for (int d = 0; d < DBW; ++d) {
+        const int ch = ((4 * (wave * DBW + d) + v_chlo) ^ v_sw) << 4;
+        const v_i16x4 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v_i16x4*)(vrow0 + ch));
+        const v_i16x4 vup = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v_i16x4*)(vrow0 + 8 * TL::ROWB + ch));
+        typedef short i16x8 __attribute__((ext_vector_type(8)));
+        const i16x8 av = __builtin_shufflevector(vlo, vup, 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[d] = VMfma<T>::run(__builtin_bit_cast(V8, av), pb, oacc[d]);
+      }
+    }
+    if (i + 1 < ntiles) {
+      store_tile(stage ^ 1, nk, nv);
+      if (i + 1 + NR < ntiles) load_tile(i + 1 + NR, nk, nv);
+    }
+    __syncthreads();  // tile i + 1 in LDS; the stage of tile i is free
+  };
+  if constexpr (NR > 2) {
+    for (int i = 0; i < ntiles; i += 3) {
+      step(i, r1k, r1v);
+      if (i + 1 < ntiles) step(i + 1, r2k, r2v);
+      if (i + 2 < ntiles) step(i + 2, r0k, r0v);
+    }
+  } else {
+    for (int i = 0; i < ntiles; i += 2) {
+      step(i, r1k, r1v);
+      if (i + 1 < ntiles) step(i + 1, r0k, r0v);
+    }
+  }
+
+  // The row's total over the two lane halves; the chunk's result: final output when the
+  // row's visible keys lie in this chunk only, else an fp32 partial (m, l, o).
+  l_run += __shfl_xor(l_run, 32, kWave);
+  if (!valid || c0 > kmax || c0 + p.chunk - 1 < kmin) return;
+  const int cmin = kmin / p.chunk, cmax = kmax / p.chunk;
+  // lane holds channels wave*DW + 32d + 8i + 4hi + j of row n
+  if (cmin == cmax) {
+    const float inv_l = 1.0f / l_run;
+    T* dst = static_cast<T*>(p.out) + b * p.sob + t * p.sot + h * p.soh + wave * TL::DW;
+#pragma unroll
+    for (int d = 0; d < DBW; ++d)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dst[32 * d + 8 * ii + 4 * hi + j] = from_f32<T>(oacc[d][4 * ii + j] * inv_l);
+  } else {
+    const int64_t rowid = ((int64_t)b * p.H + h) * p.T + t;
+    const int64_t slot = rowid * p.max_chunks + c;
+    float* dst = p.ws_o + slot * D + wave * TL::DW;
+#pragma unroll
+    for (int d = 0; d < DBW; ++d)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+        *reinterpret_cast<float4*>(dst + 32 * d + 8 * ii + 4 * hi) =
+            make_float4(oacc[d][4 * ii], oacc[d][4 * ii + 1], oacc[d][4 * ii + 2], oacc[d][4 * ii + 3]);
+    if (wave == 0 && hi == 0) p.ws_ml[slot] = make_float2(m_run, l_run);
+  }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void verify_unit(const SplitParams& p, char* smem, const int b,
+                                            const int base, const int kvh, const int rb,
+                                            const int c_in) {
+  if constexpr (D <= 256) verify_unit_staged<T, D>(p, smem, b, base, kvh, rb, c_in);
+  else verify_unit_dma<T, D>(p, smem, b, base, kvh, rb, c_in);
+}
+
+// Dynamic LDS of the MFMA verify kernels.
+template <int D> constexpr int verify_lds_bytes() {
+  return D <= 256 ? StagedTile<D <= 256 ? D : 256>::LDS_BYTES : VerifyTile<D>::LDS_BYTES;
+}
+
 // Rows of a persistent MFMA verify launch held in LDS (their first new position and the
 // prefix sums of their units): 4 KB, within the 80 KB a block may use for two blocks per CU
 // at head dim 128.
 constexpr int kVerifyPersistRows = 512;
 
 // MFMA verify kernel, dense grid: one block per (chunk, KV head x row block, batch row).
-// Waves per SIMD: two blocks per CU at head dims 128/256; at 512 one (its LDS, and the Q^T
-// operands of 32 rows, 128 registers).
-template <int D> constexpr int verify_waves_per_eu() { return D >= 512 ? 1 : 2; }
+// Waves per SIMD: two blocks per CU at head dim 128; at 256 and 512 the LDS holds one block
+// per CU, so each wave may use the whole register file (VGPRs and AGPRs) of its SIMD.
+template <int D> constexpr int verify_waves_per_eu() { return D >= 256 ? 1 : 2; }
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(verify_waves_per_eu<D>())))
@@ -1482,8 +1985,7 @@ static bool head_dim_ok(int dtype, int D) {
 // heads per KV head, whatever T is (so verify and decode of one model share it).
 // Blocks of the MFMA verify kernel one CU holds (its LDS, 160 KB per CU, is the limit).
 static int verify_blocks_per_cu(int D) {
-  const int lds = D == 512 ? VerifyTile<512>::LDS_BYTES
-                           : D == 256 ? VerifyTile<256>::LDS_BYTES : VerifyTile<128>::LDS_BYTES;
+  const int lds = D == 512 ? verify_lds_bytes<512>() : D == 256 ? verify_lds_bytes<256>() : verify_lds_bytes<128>();
   const int n = (160 * 1024) / lds;
   return n < 1 ? 1 : (n > 2 ? 2 : n);
 }
@@ -1718,13 +2220,13 @@ static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
 
 template <typename T, int D>
 static int launch_verify_d(SplitParams p, hipStream_t s) {
-  using TL = VerifyTile<D>;
+  constexpr int LDS = verify_lds_bytes<D>();
   static bool attr_set = false;  // raise the dynamic LDS limit once per kernel
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_mfma_kernel<T, D>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, TL::LDS_BYTES) != hipSuccess ||
+                            hipFuncAttributeMaxDynamicSharedMemorySize, LDS) != hipSuccess ||
         hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_mfma_persistent_kernel<T, D>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, TL::LDS_BYTES) != hipSuccess)
+                            hipFuncAttributeMaxDynamicSharedMemorySize, LDS) != hipSuccess)
       return set_error("forge_attn_decode: cannot reserve the LDS the kernel needs");
     attr_set = true;
   }
@@ -1751,9 +2253,9 @@ static int launch_verify_d(SplitParams p, hipStream_t s) {
     grid = dim3((unsigned)dense_chunks(p), (unsigned)(p.K * n_rb), (unsigned)p.B);
   }
   if (p.persist)
-    hipLaunchKernelGGL((verify_mfma_persistent_kernel<T, D>), grid, dim3(256), TL::LDS_BYTES, s, p);
+    hipLaunchKernelGGL((verify_mfma_persistent_kernel<T, D>), grid, dim3(256), LDS, s, p);
   else
-    hipLaunchKernelGGL((verify_mfma_kernel<T, D>), grid, dim3(256), TL::LDS_BYTES, s, p);
+    hipLaunchKernelGGL((verify_mfma_kernel<T, D>), grid, dim3(256), LDS, s, p);
   int st = check_launch();
   if (st || p.max_chunks < 2) return st;
   const int64_t nrows = (int64_t)p.B * p.H * p.T;
