@@ -1398,14 +1398,17 @@ template <int D> struct StagedTile {
   static constexpr int TAB_G = (4 * D + 1023) / 1024 * 1024;
   static constexpr int TAB_R = (MAX_TOK * 4 * D + 1023) / 1024 * 1024;
   static constexpr int QS_OFF = 4 * TILEB;                      // after [K0 | V0 | K1 | V1]
-  static constexpr int TAB_OFF = QS_OFF + ROWS * ROWB;
-  static constexpr int LDS_BYTES = TAB_OFF + TAB_G + 2 * TAB_R;
+  // the tables are read only by the q prologue, before tile 1 is written into stage 1: they
+  // share its bytes, so a block takes 80 KB at head dim 256 and a CU holds two
+  static constexpr int TAB_OFF = 2 * TILEB;
+  static constexpr int LDS_BYTES = QS_OFF + ROWS * ROWB;
   static constexpr bool Q_REGS = D <= 128;  // Q^T operands in registers; at 256 read per tile
   static constexpr int NCHAIN = D <= 128 ? 4 : 2;  // score accumulation chains (registers at 256)
-  static constexpr int NR = D <= 128 ? 2 : 3;      // register sets of tiles in flight
+  static constexpr int NR = 2;                     // register sets of tiles in flight
   static constexpr int DW = D / WAVES;
   static_assert(PER * THREADS * 16 == TILEB, "a tile splits into whole 16-byte pieces per thread");
   static_assert(NCH >= 16, "the K swizzle spans 16 chunks");
+  static_assert(TAB_G + 2 * TAB_R <= 2 * TILEB, "the tables fit in stage 1");
 };
 
 template <typename T, int D>
@@ -1872,9 +1875,14 @@ template <int D> constexpr int verify_lds_bytes() {
 constexpr int kVerifyPersistRows = 512;
 
 // MFMA verify kernel, dense grid: one block per (chunk, KV head x row block, batch row).
-// Waves per SIMD: two blocks per CU at head dim 128; at 256 and 512 the LDS holds one block
-// per CU, so each wave may use the whole register file (VGPRs and AGPRs) of its SIMD.
-template <int D> constexpr int verify_waves_per_eu() { return D >= 256 ? 1 : 2; }
+// Waves per SIMD: two blocks per CU at head dims 128 and 256 (the second block's waves run
+// while the first one's wait on LDS reads and dependent MFMAs: C5's global layer 29 -> xx us);
+// at 512 one (its LDS, and the Q^T operands of 32 rows, 128 registers).
+template <int D> constexpr int verify_waves_per_eu() { return D >= 512 ? 1 : 2; }
+// The persistent grid's bookkeeping (4 KB of static LDS) leaves one block per CU at 256,
+// whose waves may then use the whole register file of their SIMD.
+template <int D> constexpr int verify_persist_waves_per_eu() { return D >= 256 ? 1 : 2; }
+constexpr int kVerifyPersistStaticLds = 5 * 1024;
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(verify_waves_per_eu<D>())))
@@ -1891,12 +1899,13 @@ void verify_mfma_kernel(SplitParams p) {
 // end and the blocks that stream faster take more units. (A kernel of its own: with both
 // grids in one, the dense grid's registers grew from 150 to 212 at head dim 128.)
 template <typename T, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(verify_waves_per_eu<D>())))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(verify_persist_waves_per_eu<D>())))
 void verify_mfma_persistent_kernel(SplitParams p) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   __shared__ int sh_pref[kVerifyPersistRows + 1];
   __shared__ int sh_base[kVerifyPersistRows];
   __shared__ int sh_ticket[2];
+  static_assert(sizeof(int) * (2 * kVerifyPersistRows + 3) <= kVerifyPersistStaticLds, "bookkeeping LDS");
   const int tid = threadIdx.x;
   constexpr int ROWS = VerifyTile<D>::ROWS;
   const int per_row = p.K * ((p.rows_total + ROWS - 1) / ROWS);
@@ -1983,9 +1992,11 @@ static bool head_dim_ok(int dtype, int D) {
 
 // The MFMA path (verify_mfma_kernel) serves bf16/fp16 head dim 128/256 with G >= 4 query
 // heads per KV head, whatever T is (so verify and decode of one model share it).
-// Blocks of the MFMA verify kernel one CU holds (its LDS, 160 KB per CU, is the limit).
-static int verify_blocks_per_cu(int D) {
-  const int lds = D == 512 ? verify_lds_bytes<512>() : D == 256 ? verify_lds_bytes<256>() : verify_lds_bytes<128>();
+// Blocks of the MFMA verify kernel one CU holds (its LDS, 160 KB per CU, is the limit; the
+// persistent kernel adds its static bookkeeping).
+static int verify_blocks_per_cu(int D, bool persist = false) {
+  const int lds = (D == 512 ? verify_lds_bytes<512>() : D == 256 ? verify_lds_bytes<256>() : verify_lds_bytes<128>()) +
+                  (persist ? kVerifyPersistStaticLds : 0);
   const int n = (160 * 1024) / lds;
   return n < 1 ? 1 : (n > 2 ? 2 : n);
 }
@@ -2022,17 +2033,20 @@ static int verify_round_chunk(int B, int H, int K, int D, int64_t max_kv_len) {
   const int G = H / K;
   const int64_t pairs = (int64_t)B * K * ((G * T + kVerifyRows - 1) / kVerifyRows);
   const int64_t len = max_kv_len > 0 ? max_kv_len : 1;
-  const int64_t slots = (int64_t)verify_blocks_per_cu(D) * device_cus();
+  // At head dim 256 a CU holds two blocks, but one unit per CU writes half the fp32 partials
+  // (C5 global layer, 8 x 8196 keys: 288-key chunks 27.2-28.0 us per call against 30.5-30.9 at
+  // 160-192 keys, same box)
+  const int64_t slots = (int64_t)(D == 256 ? 1 : verify_blocks_per_cu(D)) * device_cus();
   const int64_t per_pair = slots / pairs > 1 ? slots / pairs : 1;  // chunks per (b, kv head, rows)
   int64_t chunk = (len + per_pair - 1) / per_pair;
   chunk = (chunk + 31) / 32 * 32;
-  // At least as many tiles as the pipeline keeps in flight: a shorter unit cannot use its
-  // prefetch and is mostly prologue (C5 window 1024: 64-key chunks 23.2 us, 96-key 20.9 us).
-  // (At head dim 512, with one tile in flight, the same three-tile minimum.)
-  constexpr int kMinTiles = VerifyTile<128>::STAGES - 1;
-  static_assert(VerifyTile<128>::STAGES == VerifyTile<256>::STAGES && VerifyTile<128>::BN == VerifyTile<256>::BN &&
-                VerifyTile<128>::BN == VerifyTile<512>::BN, "one tile shape for every head dim");
-  const int64_t min_chunk = (int64_t)kMinTiles * VerifyTile<128>::BN;
+  // A shorter unit is mostly prologue: at least two tiles where the staged pipeline keeps two
+  // in flight (C5 window 1024: 64-key chunks 14.9 us, 96-key 15.4 us, 32-key 17.3 us); three at
+  // head dim 512, whose direct loads keep one tile in flight.
+  static_assert(VerifyTile<128>::BN == StagedTile<128>::BN && VerifyTile<128>::BN == VerifyTile<512>::BN &&
+                StagedTile<256>::BN == VerifyTile<512>::BN, "one tile shape for every head dim");
+  const int min_tiles = D >= 512 ? 3 : StagedTile<128>::NR;
+  const int64_t min_chunk = (int64_t)min_tiles * VerifyTile<128>::BN;
   return (int)(chunk < min_chunk ? min_chunk : chunk);
 }
 
@@ -2238,7 +2252,7 @@ static int launch_verify_d(SplitParams p, hipStream_t s) {
   if (p.row_pos != nullptr && p.B <= kVerifyPersistRows && p.ws_ctr) {
     const int64_t upper = (int64_t)p.B * p.K * n_rb * p.max_chunks;
     if (upper >= (1LL << 31)) return set_error("forge_attn_decode: too many work units");
-    int64_t blocks = (int64_t)verify_blocks_per_cu(D) * device_cus();
+    int64_t blocks = (int64_t)verify_blocks_per_cu(D, true) * device_cus();
     if (upper < blocks) blocks = upper;
     p.persist = 1;
     grid = dim3((unsigned)blocks);
