@@ -987,6 +987,13 @@ __device__ __forceinline__ void verify_unit_dma(const SplitParams& p, char* smem
     visible_range32(base + rb * TL::ROWS / p.G, p.window, (int)p.max_len, umin, dummy);
     visible_range32(base + r_hi / p.G, p.window, (int)p.max_len, dummy, umax);
   }
+  // keys every valid row of the unit sees: the last token's first key to the first token's last
+  int kmin_all, kmax_all;
+  {
+    const int r_hi = rb * TL::ROWS + TL::ROWS - 1 < p.rows_total - 1 ? rb * TL::ROWS + TL::ROWS - 1 : p.rows_total - 1;
+    visible_range32(base + r_hi / p.G, p.window, (int)p.max_len, kmin_all, dummy);
+    visible_range32(base + rb * TL::ROWS / p.G, p.window, (int)p.max_len, dummy, kmax_all);
+  }
   const int c = p.span_chunks ? umin / p.chunk + c_in : c_in;  // absolute chunk
   const int c0 = c * p.chunk;
   if (c >= p.max_chunks || c0 > umax || c0 + p.chunk - 1 < umin) return;  // block-uniform
@@ -1300,16 +1307,21 @@ __device__ __forceinline__ void verify_unit_dma(const SplitParams& p, char* smem
 #pragma unroll
     for (int x = 0; x < 16; ++x) sacc[x] = (sc[0][x] + sc[1][x]) + (sc[2][x] + sc[3][x]);
 
-    // element x of this lane is key key0 + 8(x/4) + 4hi + x%4 of row n
-    const int lo = kmin - key0 - 4 * hi, top = kmax - key0 - 4 * hi;
+    // element x of this lane is key key0 + 8(x/4) + 4hi + x%4 of row n; tiles every valid
+    // row sees whole skip the mask (as in verify_unit_staged, the same values either way)
     float mx = kNegInf;
+    const bool whole = key0 >= kmin_all && key0 + BN - 1 <= kmax_all;
+    if (!whole) {
+      const int lo = kmin - key0 - 4 * hi, top = kmax - key0 - 4 * hi;
 #pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const int ce = 8 * (x >> 2) + (x & 3);
-      sacc[x] = (ce >= lo && ce <= top) ? sacc[x] * cl2 : kNegInf;
-      mx = fmaxf(mx, sacc[x]);
+      for (int x = 0; x < 16; ++x) {
+        const int ce = 8 * (x >> 2) + (x & 3);
+        sacc[x] = (ce >= lo && ce <= top) ? sacc[x] : kNegInf;
+      }
     }
-    mx = max_xor32(mx);
+#pragma unroll
+    for (int x = 0; x < 16; ++x) mx = fmaxf(mx, sacc[x]);
+    mx = max_xor32(mx) * cl2;
     if (mx > m_run + kRescaleLog2) {  // (m = -inf: first visible key)
       const float alpha = m_run == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(m_run - mx);
       l_run *= alpha;
@@ -1319,12 +1331,22 @@ __device__ __forceinline__ void verify_unit_dma(const SplitParams& p, char* smem
         for (int x = 0; x < 16; ++x) oacc[d][x] *= alpha;
       m_run = mx;
     }
+    const float neg_m = -m_run;
     float rs = 0.0f;
+    if (whole) {
 #pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const float pv = sacc[x] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(sacc[x] - m_run);
-      sacc[x] = pv;
-      rs += pv;
+      for (int x = 0; x < 16; ++x) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[x], cl2, neg_m));
+        sacc[x] = pv;
+        rs += pv;
+      }
+    } else {
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        const float pv = sacc[x] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(fmaf(sacc[x], cl2, neg_m));
+        sacc[x] = pv;
+        rs += pv;
+      }
     }
     l_run += rs;
 
