@@ -1631,17 +1631,17 @@ __device__ __forceinline__ void verify_unit_staged(const SplitParams& p, char* s
   // below its share of the HBM bandwidth)
   constexpr int NR = TL::NR;
   u4 r0k[TL::PER], r0v[TL::PER], r1k[TL::PER], r1v[TL::PER], r2k[NR > 2 ? TL::PER : 1], r2v[NR > 2 ? TL::PER : 1];
-  // The tables (and the q rows, issued before them) are waited for before the first tile is
-  // requested: every block of the launch requests its q rows at once, and tile requests
-  // issued with them would put each block's q behind the whole launch's first tiles (5 us
-  // at C5's global layer against about one round trip alone).
+  // Tile 0 goes out with the q rows and tables; the later tiles wait for them: every block
+  // of the launch requests its q rows at once, and more tile requests issued with them
+  // would put each block's q behind the whole launch's first tiles (5 us at C5's global
+  // layer with three tiles, against about one round trip alone).
+  load_tile(0, r0k, r0v);
 #pragma unroll
   for (int ps = 0; ps < NPASS; ++ps) {
     const int r = ps * RPP + tid / V4R;
     if (r < nrow) *reinterpret_cast<float4*>(tab + tab_dst(r) + tx) = tv[ps];
   }
   __builtin_amdgcn_sched_barrier(0);
-  load_tile(0, r0k, r0v);
   if (ntiles > 1) load_tile(1, r1k, r1v);
   if constexpr (NR > 2) {
     if (ntiles > 2) load_tile(2, r2k, r2v);
