@@ -532,15 +532,21 @@ struct WideTile {
   static constexpr int LDS_BYTES = STAGES * 2 * TILEB + PART_BYTES + SS_BYTES;
 };
 
-template <typename T>
+template <typename T, int SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 void prefill_wide_kernel(PrefillParams p) {
   using V8 = typename Mfma<T>::vec;
   using TL = WideTile;
   constexpr int D = TL::D;
   constexpr int BN = TL::BN;
-  constexpr int KSTEPS = 8;    // 16-channel MFMA k-steps over a wave's 128 channels
-  constexpr int DB = 4;        // 32-channel output blocks per wave
+  // SPLIT waves share a head, each with D / SPLIT channels; the block takes WAVES / SPLIT heads
+  // of one KV head, so each K/V tile is loaded once for all of them
+  static_assert(SPLIT == 4 || SPLIT == 2, "four quarter-slices of one head, or two halves of two");
+  constexpr int HPB = TL::WAVES / SPLIT;     // heads per block
+  constexpr int CW = D / SPLIT;              // channels per wave
+  constexpr int CCH = CW / 8;                // 16-byte chunks per wave slice
+  constexpr int KSTEPS = CW / 16;            // 16-channel MFMA k-steps over a wave's channels
+  constexpr int DB = CW / 32;                // 32-channel output blocks per wave
   constexpr int HALVES = BN / 16;
 
   extern __shared__ __attribute__((aligned(1024))) char smem[];
@@ -553,12 +559,16 @@ void prefill_wide_kernel(PrefillParams p) {
   const int n = lane & 31;
   const int hi = lane >> 5;
 
-  // block -> (query tile, head, batch), heavy (late) causal tiles first
-  const int HB = p.H * p.B;
+  // block -> (query tile, head group, batch), heavy (late) causal tiles first; wave w takes
+  // slice w % SPLIT of head HPB * hg + w / SPLIT
+  const int HB = (p.H / HPB) * p.B;
   const int qt = p.nqt - 1 - (int)blockIdx.x / HB;
   const int hb = (int)blockIdx.x % HB;
-  const int b = hb % p.B, h = hb / p.B;
+  const int b = hb % p.B;
+  const int slice = wave % SPLIT;
+  const int h = (hb / p.B) * HPB + wave / SPLIT;
   const int kvh = h / p.G;
+  const int wbase = wave - slice;  // the head's first wave
 
   const int i_q = qt * TL::BM + n;
   const bool valid_q = i_q < p.T;
@@ -598,32 +608,50 @@ void prefill_wide_kernel(PrefillParams p) {
   };
   issue(kt_begin, 0);
 
-  // ---- Q^T slice: channels 128 wave + 16 s + 8 hi + e, RMSNorm over all 512 channels
-  // (slice sums added through LDS in wave order), RoPE with the partner c ^ 256.
+  // ---- Q^T slice: channels CW slice + 16 s + 8 hi + e, RMSNorm over all 512 channels
+  // (slice sums added through LDS in slice order), RoPE with the partner c ^ 256.
   V8 qreg[KSTEPS];
   {
-    const int c0 = 128 * wave + 8 * hi;
-    const int pc0 = 128 * (wave ^ 2) + 8 * hi;   // partner channels
-    float x[KSTEPS][8], z[KSTEPS][8];
+    const int c0 = CW * slice + 8 * hi;
+    const int pc0 = (CW * slice + 8 * hi) ^ 256;   // partner channels
+    // raw slices stay packed (16 bf16/fp16 values per k-step in 8 registers); each k-step is
+    // unpacked, normalised, rotated and rounded in turn
+    uint4 rx[KSTEPS], rz[KSTEPS];
     const T* src = static_cast<const T*>(p.q) + b * p.sqb + h * p.sqh + (int64_t)(valid_q ? i_q : 0) * p.sqt;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
-      unpack16<T>(load16(src + c0 + 16 * s), x[s]);
-      unpack16<T>(load16(src + pc0 + 16 * s), z[s]);
+      rx[s] = load16(src + c0 + 16 * s);
+      rz[s] = load16(src + pc0 + 16 * s);
     }
-    if (p.flags & FORGE_NORM_QK) {
+    const bool norm = (p.flags & FORGE_NORM_QK) != 0;
+    float rs = 1.0f;
+    if (norm) {
       float ss = 0.0f;
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s)
+      for (int s = 0; s < KSTEPS; ++s) {
+        float x[8];
+        unpack16<T>(rx[s], x);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ss += x[s][e] * x[s][e];
+        for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+      }
       ss += __shfl_xor(ss, 32, kWave);
       if (hi == 0) sh_ss[wave * 32 + n] = ss;
       __syncthreads();
-      const float tot = ((sh_ss[n] + sh_ss[32 + n]) + sh_ss[64 + n]) + sh_ss[96 + n];
-      const float rs = rsqrtf(tot / (float)D + p.eps);
+      float tot = sh_ss[wbase * 32 + n];
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
+      for (int w = 1; w < SPLIT; ++w) tot += sh_ss[(wbase + w) * 32 + n];
+      rs = rsqrtf(tot / (float)D + p.eps);
+    }
+    const bool rope = (p.flags & FORGE_ROPE) && valid_q;
+    const float* cr = rope ? p.cos + (int64_t)i_q * p.cst : nullptr;
+    const float* sr = rope ? p.sin + (int64_t)i_q * p.cst : nullptr;
+    const bool first_half = CW * slice < 256;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      float x[8], z[8];
+      unpack16<T>(rx[s], x);
+      unpack16<T>(rz[s], z);
+      if (norm) {
         float wx[8], wz[8];
         if (p.qw) {
           load_f32x8(p.qw + c0 + 16 * s, wx);
@@ -631,33 +659,24 @@ void prefill_wide_kernel(PrefillParams p) {
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          x[s][e] *= rs;
-          z[s][e] *= rs;
+          x[e] *= rs;
+          z[e] *= rs;
           if (p.qw) {
-            x[s][e] *= wx[e];
-            z[s][e] *= wz[e];
+            x[e] *= wx[e];
+            z[e] *= wz[e];
           }
         }
       }
-    }
-    if ((p.flags & FORGE_ROPE) && valid_q) {
-      const float* cr = p.cos + (int64_t)i_q * p.cst;
-      const float* sr = p.sin + (int64_t)i_q * p.cst;
-      const bool first_half = wave < 2;
-#pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
+      if (rope) {
         float cv[8], sv[8];
         load_f32x8(cr + c0 + 16 * s, cv);
         load_f32x8(sr + c0 + 16 * s, sv);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          x[s][e] = first_half ? x[s][e] * cv[e] - z[s][e] * sv[e] : x[s][e] * cv[e] + z[s][e] * sv[e];
+        for (int e = 0; e < 8; ++e) x[e] = first_half ? x[e] * cv[e] - z[e] * sv[e] : x[e] * cv[e] + z[e] * sv[e];
       }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qreg[s][e] = from_f32<T>(valid_q ? x[e] : 0.0f);
     }
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qreg[s][e] = from_f32<T>(valid_q ? x[s][e] : 0.0f);
   }
 
   const int off = (int)p.offset;
@@ -694,7 +713,7 @@ void prefill_wide_kernel(PrefillParams p) {
     for (int x = 0; x < 16; ++x) sp[x] = 0.0f;
 #pragma unroll
     for (int st = 0; st < KSTEPS; ++st) {
-      const V8 a = *reinterpret_cast<const V8*>(kl + ((16 * wave + ((2 * st + hi) ^ k_sw)) << 4));
+      const V8 a = *reinterpret_cast<const V8*>(kl + ((CCH * slice + ((2 * st + hi) ^ k_sw)) << 4));
       sp = Mfma<T>::run(a, qreg[st], sp);
     }
     {
@@ -705,17 +724,22 @@ void prefill_wide_kernel(PrefillParams p) {
     __syncthreads();
     floatx16 sacc;
     {
-      float4 pw[4][4];
-#pragma unroll
-      for (int w = 0; w < 4; ++w)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pw[w][i] = reinterpret_cast<const float4*>(part + (w * 64 + lane) * 16)[i];
+      // the head's slices added in slice order (the same sums in every wave of the head)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sacc[4 * i + 0] = ((pw[0][i].x + pw[1][i].x) + pw[2][i].x) + pw[3][i].x;
-        sacc[4 * i + 1] = ((pw[0][i].y + pw[1][i].y) + pw[2][i].y) + pw[3][i].y;
-        sacc[4 * i + 2] = ((pw[0][i].z + pw[1][i].z) + pw[2][i].z) + pw[3][i].z;
-        sacc[4 * i + 3] = ((pw[0][i].w + pw[1][i].w) + pw[2][i].w) + pw[3][i].w;
+        float4 t = reinterpret_cast<const float4*>(part + (wbase * 64 + lane) * 16)[i];
+#pragma unroll
+        for (int w = 1; w < SPLIT; ++w) {
+          const float4 u = reinterpret_cast<const float4*>(part + ((wbase + w) * 64 + lane) * 16)[i];
+          t.x += u.x;
+          t.y += u.y;
+          t.z += u.z;
+          t.w += u.w;
+        }
+        sacc[4 * i + 0] = t.x;
+        sacc[4 * i + 1] = t.y;
+        sacc[4 * i + 2] = t.z;
+        sacc[4 * i + 3] = t.w;
       }
     }
 
@@ -768,7 +792,7 @@ void prefill_wide_kernel(PrefillParams p) {
       const char* vrow0 = vl + (16 * hf + v_row) * TL::ROWB + v_byte;
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
-        const int ch = (16 * wave + ((4 * d + v_chlo) ^ v_sw)) << 4;
+        const int ch = (CCH * slice + ((4 * d + v_chlo) ^ v_sw)) << 4;
         const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) i16x4*)(vrow0 + ch));
         const i16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -783,7 +807,7 @@ void prefill_wide_kernel(PrefillParams p) {
   l_run += __shfl_xor(l_run, 32, kWave);
   if (!valid_q) return;
   const float inv_l = 1.0f / l_run;
-  T* dst = static_cast<T*>(p.out) + b * p.sob + (int64_t)i_q * p.sot + h * p.soh + 128 * wave;
+  T* dst = static_cast<T*>(p.out) + b * p.sob + (int64_t)i_q * p.sot + h * p.soh + CW * slice;
 #pragma unroll
   for (int d = 0; d < DB; ++d)
 #pragma unroll
@@ -795,21 +819,29 @@ void prefill_wide_kernel(PrefillParams p) {
     }
 }
 
-template <typename T>
-static int launch_prefill_wide(PrefillParams p, hipStream_t s) {
+template <typename T, int SPLIT>
+static int launch_prefill_wide_s(PrefillParams p, hipStream_t s) {
   using TL = WideTile;
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_wide_kernel<T>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_wide_kernel<T, SPLIT>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, TL::LDS_BYTES) != hipSuccess)
       return set_error("forge_attn_prefill: cannot reserve the LDS the kernel needs");
     attr_set = true;
   }
+  constexpr int HPB = TL::WAVES / SPLIT;
   p.nqt = (p.T + TL::BM - 1) / TL::BM;
-  if ((int64_t)p.nqt * p.H * p.B > 0x7fffffff) return set_error("grid too large");
-  const dim3 grid((unsigned)((int64_t)p.nqt * p.H * p.B));
-  hipLaunchKernelGGL((prefill_wide_kernel<T>), grid, dim3(TL::WAVES * 64), TL::LDS_BYTES, s, p);
+  if ((int64_t)p.nqt * (p.H / HPB) * p.B > 0x7fffffff) return set_error("grid too large");
+  const dim3 grid((unsigned)((int64_t)p.nqt * (p.H / HPB) * p.B));
+  hipLaunchKernelGGL((prefill_wide_kernel<T, SPLIT>), grid, dim3(TL::WAVES * 64), TL::LDS_BYTES, s, p);
   return check_launch();
+}
+
+// Two heads of one KV head per block (head dim in halves) where the group is even: each K/V
+// tile is loaded once for both; else one head per block in quarter slices.
+template <typename T>
+static int launch_prefill_wide(PrefillParams p, hipStream_t s) {
+  return p.G % 2 == 0 ? launch_prefill_wide_s<T, 2>(p, s) : launch_prefill_wide_s<T, 4>(p, s);
 }
 
 template <typename T>

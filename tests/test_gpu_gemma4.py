@@ -82,6 +82,14 @@ def test_prefill_head_dim_512_gqa_and_documents():
     assert max_abs(got, ref) <= 2e-2
 
 
+@pytest.mark.parametrize("H,K,window", [(3, 1, 0), (2, 2, 0), (3, 1, 48)])
+def test_prefill_head_dim_512_odd_groups(H, K, window):
+    """An odd number of q heads per KV head takes the kernel's one-head-per-block form (the head
+    dim in four slices); an even one shares each K/V tile between two heads (the tests above)."""
+    got, ref = _prefill_case(11, torch.bfloat16, 2, H, K, 150, 0, window)
+    assert max_abs(got, ref) <= 2e-2
+
+
 def test_prefill_head_dim_512_downstream_argmax():
     got, ref = _prefill_case(9, torch.bfloat16, 1, 16, 1, 256, 0, 0)
     r = downstream_argmax(got, ref)
