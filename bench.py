@@ -517,7 +517,7 @@ def main() -> int:
     g4_prefill = {"config": "1 x 4096 causal, 16 q / 1 kv heads, head dim 512, bf16, QK-norm, RoPE theta 1e6",
                   "us": round(t_g4 * 1e6, 2), "TFLOPs": round(pg.flops() / t_g4 / 1e12, 1),
                   "frac": round(pg.flops() / t_g4 / 1e12 / BF16_PEAK_TFLOPS, 4),
-                  "kernel": "forge::prefill_wide_kernel<bf16>", "traffic": read_traffic("prefill_g4full_traffic")}
+                  "kernel": "forge::prefill_wide_kernel<bf16, 2>", "traffic": read_traffic("prefill_g4full_traffic")}
     print(f"[bench] Gemma-4 full-layer prefill (hd 512): {g4_prefill}", file=sys.stderr, flush=True)
     del pg
     torch.cuda.empty_cache()
