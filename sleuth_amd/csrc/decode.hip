@@ -1424,9 +1424,12 @@ template <int D> struct StagedTile {
   // share its bytes, so a block takes 80 KB at head dim 256 and a CU holds two
   static constexpr int TAB_OFF = 2 * TILEB;
   static constexpr int LDS_BYTES = QS_OFF + ROWS * ROWB;
-  static constexpr bool Q_REGS = D <= 128;  // Q^T operands in registers; at 256 read per tile
-  static constexpr int NCHAIN = D <= 128 ? 4 : 2;  // score accumulation chains (registers at 256)
+  static constexpr bool Q_REGS = D <= 128;  // Q^T operands in registers; at 256/512 read per tile
+  // score accumulation chains: two at 256 (two waves per SIMD, registers short); four at 512
+  // (one wave per SIMD), summed as verify_unit_dma sums its four, so both forms give the same bits
+  static constexpr int NCHAIN = D == 256 ? 2 : 4;
   static constexpr int NR = 2;                     // register sets of tiles in flight
+  static constexpr bool SPLIT_S = D >= 512;        // score tile split over the waves by k-steps
   static constexpr int DW = D / WAVES;
   static_assert(PER * THREADS * 16 == TILEB, "a tile splits into whole 16-byte pieces per thread");
   static_assert(NCH >= 16, "the K swizzle spans 16 chunks");
@@ -1720,11 +1723,23 @@ __device__ __forceinline__ void verify_unit_staged(const SplitParams& p, char* s
   const char* q_rd = qs_b + n * TL::ROWB;
   const int q_sw = n & 15;
   auto qop = [&](int s) { return *reinterpret_cast<const V8*>(q_rd + (((2 * s + hi) ^ q_sw) << 4)); };
-  V8 qreg[TL::Q_REGS ? KSTEPS : 1];
+  // At head dim 512 the score tile is split over the waves by k-steps: wave w computes chain
+  // w of verify_unit_dma's four (k-steps w, w + 4, ...), holds only those Q^T operands, and
+  // the four partial tiles meet in LDS (the q rows' bytes, free once every wave holds its
+  // operands) and are added as verify_unit_dma adds its chains, so both forms give the same
+  // bits. A wave then reads 8 rather than 32 K operands per tile and issues 8 score MFMAs.
+  constexpr bool SPLIT_S = TL::SPLIT_S;
+  constexpr int QR = TL::Q_REGS ? KSTEPS : SPLIT_S ? KSTEPS / TL::WAVES : 1;
+  V8 qreg[QR];
   if constexpr (TL::Q_REGS) {
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) qreg[s] = qop(s);
+  } else if constexpr (SPLIT_S) {
+#pragma unroll
+    for (int j = 0; j < QR; ++j) qreg[j] = qop(wave + TL::WAVES * j);
+    __syncthreads();  // every wave holds its operands: the q rows' bytes take the partial tiles
   }
+  char* part = smem + TL::QS_OFF;  // [wave][4][64 lanes] float4 partial score tiles
 
   // LDS read offsets within a tile (as verify_unit_dma's)
   const int k_rd = n * TL::ROWB;
@@ -1758,37 +1773,74 @@ __device__ __forceinline__ void verify_unit_staged(const SplitParams& p, char* s
     // register sets), so the LDS latency hides under two MFMAs; the scheduling groups pin
     // that order (left alone, the compiler reads each step's operands just before its MFMA
     // and waits for them: one LDS round trip per MFMA).
-    v_floatx16 sc[TL::NCHAIN];
+    v_floatx16 sacc;
+    if constexpr (SPLIT_S) {
+      v_floatx16 sw;
 #pragma unroll
-    for (int j = 0; j < TL::NCHAIN; ++j)
-#pragma unroll
-      for (int x = 0; x < 16; ++x) sc[j][x] = 0.0f;
-    {
-      constexpr int RD = TL::Q_REGS ? 1 : 2;  // LDS reads per k-step
+      for (int x = 0; x < 16; ++x) sw[x] = 0.0f;
       auto kread = [&](int st) { return *reinterpret_cast<const V8*>(kl + (((2 * st + hi) ^ k_sw) << 4)); };
-      auto qget = [&](int st) { return TL::Q_REGS ? qreg[TL::Q_REGS ? st : 0] : qop(st); };
-      V8 k0 = kread(0), k1 = kread(1), k2 = k1;
-      V8 q0 = qget(0), q1 = qget(1), q2 = q1;
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * RD, 0);
+      V8 k0 = kread(wave), k1 = kread(wave + TL::WAVES), k2 = k1;
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-      for (int st = 0; st < KSTEPS; ++st) {
-        if (st + 2 < KSTEPS) {
-          k2 = kread(st + 2);
-          q2 = qget(st + 2);
-          __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+      for (int j = 0; j < QR; ++j) {
+        if (j + 2 < QR) {
+          k2 = kread(wave + TL::WAVES * (j + 2));
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        sc[st % TL::NCHAIN] = VMfma<T>::run(k0, q0, sc[st % TL::NCHAIN]);
+        sw = VMfma<T>::run(k0, qreg[j], sw);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         k0 = k1;
         k1 = k2;
-        q0 = q1;
-        q1 = q2;
       }
-    }
-    v_floatx16 sacc;
+      float4* pw = reinterpret_cast<float4*>(part + wave * 4096) + lane;
 #pragma unroll
-    for (int x = 0; x < 16; ++x)
-      sacc[x] = TL::NCHAIN == 4 ? (sc[0][x] + sc[1][x]) + (sc[2][x] + sc[TL::NCHAIN - 1][x]) : sc[0][x] + sc[1][x];
+      for (int qd = 0; qd < 4; ++qd) pw[64 * qd] = make_float4(sw[4 * qd], sw[4 * qd + 1], sw[4 * qd + 2], sw[4 * qd + 3]);
+      __syncthreads();  // the four partial tiles in LDS
+      v_floatx16 pt[TL::WAVES];
+#pragma unroll
+      for (int w = 0; w < TL::WAVES; ++w)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const float4 v = reinterpret_cast<const float4*>(part + w * 4096)[64 * qd + lane];
+          pt[w][4 * qd] = v.x;
+          pt[w][4 * qd + 1] = v.y;
+          pt[w][4 * qd + 2] = v.z;
+          pt[w][4 * qd + 3] = v.w;
+        }
+#pragma unroll
+      for (int x = 0; x < 16; ++x) sacc[x] = (pt[0][x] + pt[1][x]) + (pt[2][x] + pt[3][x]);
+    } else {
+      v_floatx16 sc[TL::NCHAIN];
+#pragma unroll
+      for (int j = 0; j < TL::NCHAIN; ++j)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) sc[j][x] = 0.0f;
+      {
+        constexpr int RD = TL::Q_REGS ? 1 : 2;  // LDS reads per k-step
+        auto kread = [&](int st) { return *reinterpret_cast<const V8*>(kl + (((2 * st + hi) ^ k_sw) << 4)); };
+        auto qget = [&](int st) { return TL::Q_REGS ? qreg[TL::Q_REGS ? st : 0] : qop(st); };
+        V8 k0 = kread(0), k1 = kread(1), k2 = k1;
+        V8 q0 = qget(0), q1 = qget(1), q2 = q1;
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * RD, 0);
+#pragma unroll
+        for (int st = 0; st < KSTEPS; ++st) {
+          if (st + 2 < KSTEPS) {
+            k2 = kread(st + 2);
+            q2 = qget(st + 2);
+            __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+          }
+          sc[st % TL::NCHAIN] = VMfma<T>::run(k0, q0, sc[st % TL::NCHAIN]);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          k0 = k1;
+          k1 = k2;
+          q0 = q1;
+          q1 = q2;
+        }
+      }
+#pragma unroll
+      for (int x = 0; x < 16; ++x)
+        sacc[x] = TL::NCHAIN == 4 ? (sc[0][x] + sc[1][x]) + (sc[2][x] + sc[TL::NCHAIN - 1][x]) : sc[0][x] + sc[1][x];
+    }
 
     // element x of this lane is key key0 + 8(x/4) + 4hi + x%4 of row n. A tile every valid
     // row of the unit sees whole (block-uniform) skips the mask and the masked-key tests; both
@@ -1902,17 +1954,22 @@ __device__ __forceinline__ void verify_unit_staged(const SplitParams& p, char* s
   }
 }
 
-template <typename T, int D>
+// The staged form at every head dim, except the persistent grid at 512: there the staged
+// form's 160 KB of LDS leaves no room for the grid's bookkeeping, and the direct-load form
+// (150 KB) computes the same values bit for bit.
+template <int D, bool PERSIST> constexpr bool verify_staged() { return D <= 256 || !PERSIST; }
+
+template <typename T, int D, bool PERSIST>
 __device__ __forceinline__ void verify_unit(const SplitParams& p, char* smem, const int b,
                                             const int base, const int kvh, const int rb,
                                             const int c_in) {
-  if constexpr (D <= 256) verify_unit_staged<T, D>(p, smem, b, base, kvh, rb, c_in);
+  if constexpr (verify_staged<D, PERSIST>()) verify_unit_staged<T, D>(p, smem, b, base, kvh, rb, c_in);
   else verify_unit_dma<T, D>(p, smem, b, base, kvh, rb, c_in);
 }
 
 // Dynamic LDS of the MFMA verify kernels.
-template <int D> constexpr int verify_lds_bytes() {
-  return D <= 256 ? StagedTile<D <= 256 ? D : 256>::LDS_BYTES : VerifyTile<D>::LDS_BYTES;
+template <int D, bool PERSIST> constexpr int verify_lds_bytes() {
+  return verify_staged<D, PERSIST>() ? StagedTile<D>::LDS_BYTES : VerifyTile<D>::LDS_BYTES;
 }
 
 // Rows of a persistent MFMA verify launch held in LDS (their first new position and the
@@ -1935,7 +1992,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(verify_wave
 void verify_mfma_kernel(SplitParams p) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   const int b = blockIdx.z;
-  verify_unit<T, D>(p, smem, b, (int)row_base(p.row_pos, p.pos_dev, p.pos0, b), blockIdx.y % p.K,
+  verify_unit<T, D, false>(p, smem, b, (int)row_base(p.row_pos, p.pos_dev, p.pos0, b), blockIdx.y % p.K,
                     blockIdx.y / p.K, blockIdx.x);
 }
 
@@ -2007,7 +2064,7 @@ void verify_mfma_persistent_kernel(SplitParams p) {
     int kmin, kmax;
     visible_range32(base, p.window, (int)p.max_len, kmin, kmax);  // the row's first chunk
     // a row's chunks last to first (the last one's unit also makes the new keys)
-    verify_unit<T, D>(p, smem, lo, base, pr % p.K, pr / p.K, kmin / p.chunk + (nch - 1 - o % nch));
+    verify_unit<T, D, true>(p, smem, lo, base, pr % p.K, pr / p.K, kmin / p.chunk + (nch - 1 - o % nch));
     if (tid == 0) sh_ticket[parity] = (int)gridDim.x + next;
     __syncthreads();  // the next unit reuses the LDS stages and tables; the ticket is visible
   }
@@ -2041,8 +2098,12 @@ static bool head_dim_ok(int dtype, int D) {
 // Blocks of the MFMA verify kernel one CU holds (its LDS, 160 KB per CU, is the limit; the
 // persistent kernel adds its static bookkeeping).
 static int verify_blocks_per_cu(int D, bool persist = false) {
-  const int lds = (D == 512 ? verify_lds_bytes<512>() : D == 256 ? verify_lds_bytes<256>() : verify_lds_bytes<128>()) +
-                  (persist ? kVerifyPersistStaticLds : 0);
+  const int lds = persist ? (D == 512   ? verify_lds_bytes<512, true>()
+                             : D == 256 ? verify_lds_bytes<256, true>()
+                                        : verify_lds_bytes<128, true>()) + kVerifyPersistStaticLds
+                          : (D == 512   ? verify_lds_bytes<512, false>()
+                             : D == 256 ? verify_lds_bytes<256, false>()
+                                        : verify_lds_bytes<128, false>());
   const int n = (160 * 1024) / lds;
   return n < 1 ? 1 : (n > 2 ? 2 : n);
 }
@@ -2280,13 +2341,14 @@ static int launch_split_d(SplitParams p, int rows, hipStream_t s) {
 
 template <typename T, int D>
 static int launch_verify_d(SplitParams p, hipStream_t s) {
-  constexpr int LDS = verify_lds_bytes<D>();
+  constexpr int LDS = verify_lds_bytes<D, false>();
+  constexpr int LDS_P = verify_lds_bytes<D, true>();
   static bool attr_set = false;  // raise the dynamic LDS limit once per kernel
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_mfma_kernel<T, D>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, LDS) != hipSuccess ||
         hipFuncSetAttribute(reinterpret_cast<const void*>(&verify_mfma_persistent_kernel<T, D>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, LDS) != hipSuccess)
+                            hipFuncAttributeMaxDynamicSharedMemorySize, LDS_P) != hipSuccess)
       return set_error("forge_attn_decode: cannot reserve the LDS the kernel needs");
     attr_set = true;
   }
@@ -2313,7 +2375,7 @@ static int launch_verify_d(SplitParams p, hipStream_t s) {
     grid = dim3((unsigned)dense_chunks(p), (unsigned)(p.K * n_rb), (unsigned)p.B);
   }
   if (p.persist)
-    hipLaunchKernelGGL((verify_mfma_persistent_kernel<T, D>), grid, dim3(256), LDS, s, p);
+    hipLaunchKernelGGL((verify_mfma_persistent_kernel<T, D>), grid, dim3(256), LDS_P, s, p);
   else
     hipLaunchKernelGGL((verify_mfma_kernel<T, D>), grid, dim3(256), LDS, s, p);
   int st = check_launch();

@@ -165,6 +165,27 @@ def test_verify_rows_equal_decodes_head_dim_512():
 
 
 @pytest.mark.parametrize("T", [1, 4])
+def test_decode_head_dim_512_per_row_equals_dense(T):
+    """Per-row positions (the persistent grid, tiles loaded straight into LDS) and one host
+    position (the dense grid, tiles staged through registers, the score tile split over the
+    waves) give the same bits at equal chunks, q norm and RoPE included."""
+    g = gen(31 + T)
+    B, H, K, L = 3, 16, 1, 1500
+    kc = (0.2 * randn(g, B, K, L + 4, D)).to(torch.bfloat16).to(DEV)
+    vc = randn(g, B, K, L + 4, D, dtype=torch.bfloat16).to(DEV)
+    q = randn(g, B, T, H, D, dtype=torch.bfloat16).transpose(1, 2).to(DEV)
+    w = _gain(g, torch.bfloat16).to(DEV)
+    cos_t, sin_t = tables(D, L + 4, 1e6)
+    c = cos_t[L - T:L].expand(B, T, D).contiguous().to(DEV)
+    s = sin_t[L - T:L].expand(B, T, D).contiguous().to(DEV)
+    kw = dict(scale=SCALE, q_weight=w, eps=1e-6, norm_q=True, cos=c, sin=s, chunk=256)
+    dense = ops().attn_decode(q, kc, vc, pos=L - T, **kw)
+    per_row = ops().attn_decode(q, kc, vc, row_pos=torch.full((B,), L - T, dtype=torch.int32, device=DEV),
+                                max_kv_len=L, **kw)
+    assert torch.equal(dense, per_row)
+
+
+@pytest.mark.parametrize("T", [1, 4])
 def test_decode_append_head_dim_512_equals_two_calls(T):
     """forge_attn_decode_append (v from the raw keys, values normalised without a gain, scale
     1.0) equals forge_kv_append + forge_attn_decode bit for bit, outputs and caches."""
