@@ -954,8 +954,9 @@ template <int N> __device__ __forceinline__ void vwait_vm() {
 // new token sits at position `base`), keys of chunk c_in (absolute; with p.span_chunks,
 // counted from the unit's first visible chunk). The caller passes block-uniform arguments
 // and a converged block; the unit may leave early, block-uniformly, and uses all of the
-// dynamic LDS `smem`. This form (head dim 512) fills the LDS stages with direct loads; head
-// dims 128 and 256 take verify_unit_staged below.
+// dynamic LDS `smem`. This form fills the LDS stages with direct loads; it serves head dim
+// 512 on the persistent grid (per-row positions), and verify_unit_staged below every other
+// case.
 template <typename T, int D>
 __device__ __forceinline__ void verify_unit_dma(const SplitParams& p, char* smem, const int b,
                                                 const int base, const int kvh, const int rb,
@@ -1400,13 +1401,13 @@ __device__ __forceinline__ void verify_unit_dma(const SplitParams& p, char* smem
   }
 }
 
-// Head dims 128 and 256: the K and V tiles go from HBM into registers (16-byte
-// non-temporal loads, two tiles in flight) and the threads write them into two LDS stages
-// with the same swizzled layouts. A CU streams about 23-30 GB/s through direct-to-LDS loads
-// whatever the waves and depth, against 36-48 GB/s through registers (7.3 against 5.9 TB/s
-// over the chip), and the q rows and tables, loaded first into registers, no longer queue
-// behind the tiles. LDS: two stages of K and V, the normalised q rows (chunk-swizzled by row,
-// so the Q^T operand reads are conflict-free) and the tables.
+// Head dims 128 and 256, and 512 on the dense grid: the K and V tiles go from HBM into
+// registers (16-byte non-temporal loads, two tiles in flight) and the threads write them
+// into two LDS stages with the same swizzled layouts. A CU streams about 23-30 GB/s through
+// direct-to-LDS loads whatever the waves and depth, against 36-48 GB/s through registers
+// (7.3 against 5.9 TB/s over the chip), and the q rows and tables, loaded first into
+// registers, no longer queue behind the tiles. LDS: two stages of K and V, the normalised q
+// rows (chunk-swizzled by row, so the Q^T operand reads are conflict-free) and the tables.
 template <int D> struct StagedTile {
   static constexpr int WAVES = 4;
   static constexpr int THREADS = WAVES * 64;
