@@ -137,18 +137,21 @@ def test_decode_head_dim_512_many_chunks(H):
     assert max_abs(got, ref) <= 2e-2
 
 
-@pytest.mark.parametrize("T", [1, 4])
-def test_decode_head_dim_512_host_position(T):
-    """One position for every row (the dense grid with the uniform chunk rule), 16 q heads
-    per KV head, against the oracle."""
-    g = gen(21 + T)
+@pytest.mark.parametrize("dtype,T,window", [(torch.bfloat16, 1, 0), (torch.bfloat16, 4, 0),
+                                            (torch.float16, 4, 0), (torch.bfloat16, 4, 700),
+                                            (torch.float16, 1, 100)])
+def test_decode_head_dim_512_host_position(dtype, T, window):
+    """One position for every row (the dense grid with the uniform chunk rule: tiles staged
+    through registers, the score tile split over the waves), 16 q heads per KV head, against
+    the oracle; sliding windows included."""
+    g = gen(21 + T + window)
     B, H, K, L = 4, 16, 1, 3000
-    kc = (0.2 * randn(g, B, K, L + 5, D)).to(torch.bfloat16)
-    vc = randn(g, B, K, L + 5, D, dtype=torch.bfloat16)
-    q = randn(g, B, T, H, D, dtype=torch.bfloat16).transpose(1, 2)
-    ref = oracle.ragged_decode(q.float(), kc.float(), vc.float(), [L] * B, 0, SCALE)
-    got = ops().attn_decode(q.to(DEV), kc.to(DEV), vc.to(DEV), scale=SCALE, pos=L - T)
-    assert max_abs(got.cpu(), ref.transpose(1, 2)) <= 2e-2
+    kc = (0.2 * randn(g, B, K, L + 5, D)).to(dtype)
+    vc = randn(g, B, K, L + 5, D, dtype=dtype)
+    q = randn(g, B, T, H, D, dtype=dtype).transpose(1, 2)
+    ref = oracle.ragged_decode(q.float(), kc.float(), vc.float(), [L] * B, window, SCALE)
+    got = ops().attn_decode(q.to(DEV), kc.to(DEV), vc.to(DEV), scale=SCALE, pos=L - T, window=window)
+    assert max_abs(got.cpu(), ref.transpose(1, 2)) <= tol(dtype)
 
 
 def test_verify_rows_equal_decodes_head_dim_512():
