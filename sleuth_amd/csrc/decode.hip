@@ -1425,12 +1425,15 @@ template <int D> struct StagedTile {
   // share its bytes, so a block takes 80 KB at head dim 256 and a CU holds two
   static constexpr int TAB_OFF = 2 * TILEB;
   static constexpr int LDS_BYTES = QS_OFF + ROWS * ROWB;
-  static constexpr bool Q_REGS = D <= 128;  // Q^T operands in registers; at 256/512 read per tile
+  // Q^T operands: all in registers at 128; at 256 read from the q rows in LDS per tile; at
+  // 512 the score tile is split over the waves by k-steps (SPLIT_S) and each wave holds its
+  // quarter of the operands in registers
+  static constexpr bool Q_REGS = D <= 128;
+  static constexpr bool SPLIT_S = D >= 512;
   // score accumulation chains: two at 256 (two waves per SIMD, registers short); four at 512
-  // (one wave per SIMD), summed as verify_unit_dma sums its four, so both forms give the same bits
+  // (one per wave), added as verify_unit_dma adds its four, so both forms give the same bits
   static constexpr int NCHAIN = D == 256 ? 2 : 4;
   static constexpr int NR = 2;                     // register sets of tiles in flight
-  static constexpr bool SPLIT_S = D >= 512;        // score tile split over the waves by k-steps
   static constexpr int DW = D / WAVES;
   static_assert(PER * THREADS * 16 == TILEB, "a tile splits into whole 16-byte pieces per thread");
   static_assert(NCH >= 16, "the K swizzle spans 16 chunks");
