@@ -680,6 +680,7 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
 // Grid mode (batches too large for the LDS prefix): one block per (chunk, head x row
 // block, batch row), as before.
 constexpr int kPersistMaxRows = 2048;
+constexpr int kLastClasses = 16;  // size classes of the rows' last chunks (the hand-out order)
 
 // Occupancy target: more waves hide more HBM latency, fewer leave registers for the
 // accumulators of ROWS query rows and the pipeline's buffers (the persistent grid holds two
@@ -702,9 +703,14 @@ void splitk_kernel(SplitParams p) {
   __shared__ int sh_pref[kPersistMaxRows + 1];
   __shared__ int sh_base[kPersistMaxRows];  // first new token's position of each row
   __shared__ int sh_nch[kPersistMaxRows];
+  __shared__ int sh_last[kPersistMaxRows];     // rows by the size of their last chunk, largest first
+  __shared__ unsigned char sh_cls[kPersistMaxRows];
+  __shared__ int sh_count[kLastClasses];
   const int tid = threadIdx.x;
   const int n_rb = (p.rows_total + ROWS - 1) / ROWS;
   const int per_row = p.K * n_rb;  // (kv head, row block) pairs per chunk
+  if (tid < kLastClasses) sh_count[tid] = 0;
+  __syncthreads();
   // chunk range of each batch row: union of its T queries' visible keys
   for (int b = tid; b < p.B; b += kSplitThreads) {
     const int base = (int)row_base(p.row_pos, p.pos_dev, p.pos0, b);
@@ -715,7 +721,50 @@ void splitk_kernel(SplitParams p) {
     const int cmin = lo / p.chunk;
     int cmax = hi / p.chunk;
     if (cmax > p.max_chunks - 1) cmax = p.max_chunks - 1;
-    sh_nch[b] = (hi >= lo && cmax >= cmin) ? cmax - cmin + 1 : 0;
+    const int nch = (hi >= lo && cmax >= cmin) ? cmax - cmin + 1 : 0;
+    sh_nch[b] = nch;
+    // keys of the last chunk, in kLastClasses size classes (0: none)
+    int size = 0;
+    if (nch > 0) {
+      const int c_lo = cmax * p.chunk > lo ? cmax * p.chunk : lo;
+      const int c_hi = (cmax + 1) * p.chunk - 1 < hi ? (cmax + 1) * p.chunk - 1 : hi;
+      size = c_hi - c_lo + 1;
+    }
+    const int cls = size > 0 ? (int)(((int64_t)size * kLastClasses - 1) / p.chunk) : 0;
+    sh_cls[b] = (unsigned char)cls;
+    atomicAdd(&sh_count[cls], 1);
+  }
+  __syncthreads();
+  // The rows' last chunks go out at the end, largest first: the blocks that run out of work
+  // first take the longest of them, which shortens the launch's tail. A counting sort by
+  // size class, stable (row order within a class), since every block of the launch must
+  // derive the same unit -> row map.
+  if (tid == 0) {
+    int run = 0;
+    for (int k = kLastClasses - 1; k >= 0; --k) {
+      const int c = sh_count[k];
+      sh_count[k] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  if (tid < kWave) {  // wave 0, 64 rows at a time; lane k keeps the running count of class k
+    int run = 0;
+    for (int b0 = 0; b0 < p.B; b0 += kWave) {
+      const int b = b0 + tid;
+      const int c = b < p.B ? (int)sh_cls[b] : -1;
+      unsigned long long left = __ballot(c >= 0);
+      int slot = 0;
+      while (left) {  // one pass per class present among these rows
+        const int c0 = __builtin_amdgcn_readlane(c, __builtin_ctzll(left));
+        const unsigned long long same = __ballot(c == c0);
+        const int placed = __builtin_amdgcn_readlane(run, c0);
+        if (c == c0) slot = sh_count[c0] + placed + __popcll(same & ((1ull << tid) - 1));
+        if (tid == c0) run += __popcll(same);
+        left &= ~same;
+      }
+      if (b < p.B) sh_last[slot] = b;
+    }
   }
   __syncthreads();
   // exclusive prefix sum of units per row (wave 0: lane l scans a contiguous segment)
@@ -741,10 +790,9 @@ void splitk_kernel(SplitParams p) {
   __syncthreads();
   // Units [0, body) are every row's chunks but its last, (row, KV head x row block, chunk)
   // with the chunk fastest, each row's from its second-to-last chunk down; units
-  // [body, total) are the rows' last chunks, (row, KV head x row block). A ragged batch's
-  // last chunks are partial (a random part of a chunk each), so handing them out last
-  // shortens the units left when blocks run out of work (C4 step 607.9 us against 609.7 us
-  // with each row's last chunk first, same box).
+  // [body, total) are the rows' last chunks, (row in sh_last's order, KV head x row block).
+  // A ragged batch's last chunks are partial (a random part of a chunk each), so handing
+  // them out last, largest first, shortens the units left when blocks run out of work.
   const int body = sh_pref[p.B];
   const int total = body + p.B * per_row;
   // Block i starts with unit i; after that units go by ticket (grid + an atomic counter
@@ -779,7 +827,7 @@ void splitk_kernel(SplitParams p) {
       // a row with no visible key has no last chunk either: cidx -1 lies before every key,
       // and the unit returns at once
       const int q = u - body;
-      lo = q / per_row;
+      lo = __builtin_amdgcn_readfirstlane(sh_last[q / per_row]);
       pr = q % per_row;
       cidx = __builtin_amdgcn_readfirstlane(sh_nch[lo]) - 1;
     }
