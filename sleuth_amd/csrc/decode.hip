@@ -682,6 +682,60 @@ __device__ __forceinline__ void split_unit(const SplitParams& p, const int b, co
 constexpr int kPersistMaxRows = 2048;
 constexpr int kLastClasses = 16;  // size classes of the rows' last chunks (the hand-out order)
 
+// Size class (0 .. kLastClasses - 1) of the last chunk of a row whose first new token sits at
+// `base`: the chunk holding its last visible key, cut to the row's visible keys; 0 also for
+// a row with no visible key.
+__device__ __forceinline__ int last_chunk_class(const SplitParams& p, int base) {
+  int lo, hi0, lo1, hi;
+  visible_range32(base, p.window, (int)p.max_len, lo, hi0);
+  visible_range32(base + p.T - 1, p.window, (int)p.max_len, lo1, hi);
+  const int cmin = lo / p.chunk;
+  int cmax = hi / p.chunk;
+  if (cmax > p.max_chunks - 1) cmax = p.max_chunks - 1;
+  if (hi < lo || cmax < cmin) return 0;
+  const int c_lo = cmax * p.chunk > lo ? cmax * p.chunk : lo;
+  const int c_hi = (cmax + 1) * p.chunk - 1 < hi ? (cmax + 1) * p.chunk - 1 : hi;
+  return (int)(((int64_t)(c_hi - c_lo + 1) * kLastClasses - 1) / p.chunk);
+}
+
+// The persistent grids hand out the rows' last chunks at the end, largest first: the blocks
+// that run out of work first take the longest of them, which shortens the launch's tail
+// (a ragged batch's last chunks are a random part of a chunk each). A counting sort of the
+// B rows by class (counts[] holds each class's rows, cls[] each row's class): sh_last[i] is
+// the row of the i-th last chunk. Stable (row order within a class), since every block of a
+// launch must derive the same unit -> row map. Called by the whole block.
+__device__ __forceinline__ void order_last_chunks(int B, int* counts, const unsigned char* cls, int* sh_last) {
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    int run = 0;
+    for (int k = kLastClasses - 1; k >= 0; --k) {
+      const int c = counts[k];
+      counts[k] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  if (tid < kWave) {  // wave 0, 64 rows at a time; lane k keeps the running count of class k
+    int run = 0;
+    for (int b0 = 0; b0 < B; b0 += kWave) {
+      const int b = b0 + tid;
+      const int c = b < B ? (int)cls[b] : -1;
+      unsigned long long left = __ballot(c >= 0);
+      int slot = 0;
+      while (left) {  // one pass per class present among these rows
+        const int c0 = __builtin_amdgcn_readlane(c, __builtin_ctzll(left));
+        const unsigned long long same = __ballot(c == c0);
+        const int placed = __builtin_amdgcn_readlane(run, c0);
+        if (c == c0) slot = counts[c0] + placed + __popcll(same & ((1ull << tid) - 1));
+        if (tid == c0) run += __popcll(same);
+        left &= ~same;
+      }
+      if (b < B) sh_last[slot] = b;
+    }
+  }
+  __syncthreads();
+}
+
 // Occupancy target: more waves hide more HBM latency, fewer leave registers for the
 // accumulators of ROWS query rows and the pipeline's buffers (the persistent grid holds two
 // blocks per CU, two waves per SIMD, whatever the target).
@@ -721,52 +775,13 @@ void splitk_kernel(SplitParams p) {
     const int cmin = lo / p.chunk;
     int cmax = hi / p.chunk;
     if (cmax > p.max_chunks - 1) cmax = p.max_chunks - 1;
-    const int nch = (hi >= lo && cmax >= cmin) ? cmax - cmin + 1 : 0;
-    sh_nch[b] = nch;
-    // keys of the last chunk, in kLastClasses size classes (0: none)
-    int size = 0;
-    if (nch > 0) {
-      const int c_lo = cmax * p.chunk > lo ? cmax * p.chunk : lo;
-      const int c_hi = (cmax + 1) * p.chunk - 1 < hi ? (cmax + 1) * p.chunk - 1 : hi;
-      size = c_hi - c_lo + 1;
-    }
-    const int cls = size > 0 ? (int)(((int64_t)size * kLastClasses - 1) / p.chunk) : 0;
+    sh_nch[b] = (hi >= lo && cmax >= cmin) ? cmax - cmin + 1 : 0;
+    const int cls = last_chunk_class(p, base);
     sh_cls[b] = (unsigned char)cls;
     atomicAdd(&sh_count[cls], 1);
   }
   __syncthreads();
-  // The rows' last chunks go out at the end, largest first: the blocks that run out of work
-  // first take the longest of them, which shortens the launch's tail. A counting sort by
-  // size class, stable (row order within a class), since every block of the launch must
-  // derive the same unit -> row map.
-  if (tid == 0) {
-    int run = 0;
-    for (int k = kLastClasses - 1; k >= 0; --k) {
-      const int c = sh_count[k];
-      sh_count[k] = run;
-      run += c;
-    }
-  }
-  __syncthreads();
-  if (tid < kWave) {  // wave 0, 64 rows at a time; lane k keeps the running count of class k
-    int run = 0;
-    for (int b0 = 0; b0 < p.B; b0 += kWave) {
-      const int b = b0 + tid;
-      const int c = b < p.B ? (int)sh_cls[b] : -1;
-      unsigned long long left = __ballot(c >= 0);
-      int slot = 0;
-      while (left) {  // one pass per class present among these rows
-        const int c0 = __builtin_amdgcn_readlane(c, __builtin_ctzll(left));
-        const unsigned long long same = __ballot(c == c0);
-        const int placed = __builtin_amdgcn_readlane(run, c0);
-        if (c == c0) slot = sh_count[c0] + placed + __popcll(same & ((1ull << tid) - 1));
-        if (tid == c0) run += __popcll(same);
-        left &= ~same;
-      }
-      if (b < p.B) sh_last[slot] = b;
-    }
-  }
-  __syncthreads();
+  order_last_chunks(p.B, sh_count, sh_cls, sh_last);
   // exclusive prefix sum of units per row (wave 0: lane l scans a contiguous segment)
   if (tid < kWave) {
     const int seg = (p.B + kWave - 1) / kWave;
@@ -2024,20 +2039,20 @@ template <int D, bool PERSIST> constexpr int verify_lds_bytes() {
   return verify_staged<D, PERSIST>() ? StagedTile<D>::LDS_BYTES : VerifyTile<D>::LDS_BYTES;
 }
 
-// Rows of a persistent MFMA verify launch held in LDS (their first new position and the
-// prefix sums of their units): 4 KB, within the 80 KB a block may use for two blocks per CU
-// at head dim 128.
+// Rows of a persistent MFMA verify launch held in LDS (their first new position, the prefix
+// sums of their units and the hand-out order of their last chunks): under 8 KB, within the
+// 80 KB a block may use for two blocks per CU at head dim 128.
 constexpr int kVerifyPersistRows = 512;
 
 // MFMA verify kernel, dense grid: one block per (chunk, KV head x row block, batch row).
-// Waves per SIMD: two blocks per CU at head dims 128 and 256 (the second block's waves run
-// while the first one's wait on LDS reads and dependent MFMAs: C5's global layer 29 -> xx us);
-// at 512 one (its LDS, and the Q^T operands of 32 rows, 128 registers).
+// Waves per SIMD: two at head dims 128 and 256, so a CU may hold two blocks (the second
+// block's waves run while the first one's wait on LDS reads and dependent MFMAs); at 512 one
+// (160 KB of LDS per block, and two register sets of 32 KB tiles per wave).
 template <int D> constexpr int verify_waves_per_eu() { return D >= 512 ? 1 : 2; }
-// The persistent grid's bookkeeping (4 KB of static LDS) leaves one block per CU at 256,
+// The persistent grid's bookkeeping (under 8 KB of static LDS) leaves one block per CU at 256,
 // whose waves may then use the whole register file of their SIMD.
 template <int D> constexpr int verify_persist_waves_per_eu() { return D >= 256 ? 1 : 2; }
-constexpr int kVerifyPersistStaticLds = 5 * 1024;
+constexpr int kVerifyPersistStaticLds = 8 * 1024;
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(verify_waves_per_eu<D>())))
@@ -2059,8 +2074,12 @@ void verify_mfma_persistent_kernel(SplitParams p) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   __shared__ int sh_pref[kVerifyPersistRows + 1];
   __shared__ int sh_base[kVerifyPersistRows];
+  __shared__ int sh_last[kVerifyPersistRows];
+  __shared__ unsigned char sh_cls[kVerifyPersistRows];
+  __shared__ int sh_count[kLastClasses];
   __shared__ int sh_ticket[2];
-  static_assert(sizeof(int) * (2 * kVerifyPersistRows + 3) <= kVerifyPersistStaticLds, "bookkeeping LDS");
+  static_assert(sizeof(int) * (3 * kVerifyPersistRows + kLastClasses + 3) + kVerifyPersistRows <=
+                    kVerifyPersistStaticLds, "bookkeeping LDS");
   const int tid = threadIdx.x;
   constexpr int ROWS = VerifyTile<D>::ROWS;
   const int per_row = p.K * ((p.rows_total + ROWS - 1) / ROWS);
@@ -2074,14 +2093,28 @@ void verify_mfma_persistent_kernel(SplitParams p) {
     if (cmax > p.max_chunks - 1) cmax = p.max_chunks - 1;
     return (hi >= lo && cmax >= cmin) ? cmax - cmin + 1 : 0;
   };
-  for (int b = tid; b < p.B; b += blockDim.x) sh_base[b] = (int)row_base(p.row_pos, p.pos_dev, p.pos0, b);
+  if (tid < kLastClasses) sh_count[tid] = 0;
   __syncthreads();
+  for (int b = tid; b < p.B; b += blockDim.x) {
+    const int base = (int)row_base(p.row_pos, p.pos_dev, p.pos0, b);
+    sh_base[b] = base;
+    const int cls = last_chunk_class(p, base);
+    sh_cls[b] = (unsigned char)cls;
+    atomicAdd(&sh_count[cls], 1);
+  }
+  __syncthreads();
+  // units [0, body): every row's chunks but its last, (row, KV head x row block, chunk) with
+  // the chunk fastest, each row's from its second-to-last chunk down; [body, total): the
+  // rows' last chunks, largest first (as in splitk_kernel)
   if (tid < kWave) {
     const int seg = (p.B + kWave - 1) / kWave;
     const int r0 = tid * seg;
     const int r1 = r0 + seg < p.B ? r0 + seg : p.B;
     int sum = 0;
-    for (int r = r0; r < r1; ++r) sum += row_chunks(sh_base[r]) * per_row;
+    for (int r = r0; r < r1; ++r) {
+      const int n = row_chunks(sh_base[r]);
+      sum += (n > 0 ? n - 1 : 0) * per_row;
+    }
     int incl = sum;
 #pragma unroll
     for (int d = 1; d < kWave; d <<= 1) {
@@ -2091,32 +2124,45 @@ void verify_mfma_persistent_kernel(SplitParams p) {
     int run = incl - sum;
     for (int r = r0; r < r1; ++r) {
       sh_pref[r] = run;
-      run += row_chunks(sh_base[r]) * per_row;
+      const int n = row_chunks(sh_base[r]);
+      run += (n > 0 ? n - 1 : 0) * per_row;
     }
     if (tid == kWave - 1) sh_pref[p.B] = incl;
   }
-  __syncthreads();
-  const int total = sh_pref[p.B];
+  order_last_chunks(p.B, sh_count, sh_cls, sh_last);
+  const int body = sh_pref[p.B];
+  const int total = body + p.B * per_row;
   // Block i starts with unit i, then takes units by ticket; the ticket slots alternate, as
   // in splitk_kernel (a unit may leave without a block barrier).
   int parity = 0;
   for (int u = blockIdx.x; u < total; u = __builtin_amdgcn_readfirstlane(sh_ticket[parity]), parity ^= 1) {
     int next = 0;
     if (tid == 0) next = atomicAdd(p.ws_ctr, 1);  // read after the unit: its round trip hides
-    int lo = 0, hi = p.B - 1;  // last row with sh_pref[row] <= u
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (__builtin_amdgcn_readfirstlane(sh_pref[mid]) <= u) lo = mid;
-      else hi = mid - 1;
+    int lo, pr, cidx;  // row, (KV head, row block), chunk counted from the row's first
+    if (u < body) {
+      lo = 0;
+      int hi = p.B - 1;  // last row with sh_pref[row] <= u
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (__builtin_amdgcn_readfirstlane(sh_pref[mid]) <= u) lo = mid;
+        else hi = mid - 1;
+      }
+      const int o = u - __builtin_amdgcn_readfirstlane(sh_pref[lo]);
+      const int n = row_chunks(__builtin_amdgcn_readfirstlane(sh_base[lo])) - 1;  // >= 1 here
+      pr = o / n;
+      cidx = n - 1 - o % n;
+    } else {
+      // a row with no visible key has no last chunk either: cidx -1 lies before every key,
+      // and the unit returns at once
+      const int q = u - body;
+      lo = __builtin_amdgcn_readfirstlane(sh_last[q / per_row]);
+      pr = q % per_row;
+      cidx = row_chunks(__builtin_amdgcn_readfirstlane(sh_base[lo])) - 1;
     }
     const int base = __builtin_amdgcn_readfirstlane(sh_base[lo]);
-    const int o = u - __builtin_amdgcn_readfirstlane(sh_pref[lo]);
-    const int nch = row_chunks(base);
-    const int pr = o / nch;
     int kmin, kmax;
     visible_range32(base, p.window, (int)p.max_len, kmin, kmax);  // the row's first chunk
-    // a row's chunks last to first (the last one's unit also makes the new keys)
-    verify_unit<T, D, true>(p, smem, lo, base, pr % p.K, pr / p.K, kmin / p.chunk + (nch - 1 - o % nch));
+    verify_unit<T, D, true>(p, smem, lo, base, pr % p.K, pr / p.K, kmin / p.chunk + cidx);
     if (tid == 0) sh_ticket[parity] = (int)gridDim.x + next;
     __syncthreads();  // the next unit reuses the LDS stages and tables; the ticket is visible
   }
