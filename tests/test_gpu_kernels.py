@@ -298,6 +298,20 @@ def test_decode_ragged_many_rows(B):
     assert max_abs(got, ref) <= 2e-2
 
 
+@pytest.mark.parametrize("B,H,K,D,T,window", [(1000, 4, 2, 64, 1, 0), (2048, 2, 2, 32, 2, 0),
+                                                (200, 16, 4, 128, 3, 0), (512, 8, 2, 128, 1, 90)])
+def test_persistent_tail_order_many_rows(B, H, K, D, T, window):
+    """The persistent grids hand the rows' last chunks out last, largest first, in an order
+    every block derives alike (a stable counting sort by size class, in passes of 64 rows).
+    Many rows, many of one class (lengths repeat): the split kernel up to its 2048-row limit
+    and the MFMA kernel (G = 4) up to its 512, against the oracle."""
+    rng = random.Random(B + T)
+    lens = [rng.choice([T, 97, 128, 129, 256, 300, rng.randint(T, 600)]) for _ in range(B)]
+    lens = [max(L, T) for L in lens]
+    got, ref = _decode_case(B + 17, torch.bfloat16, B, H, K, D, T, lens, window, chunk=128)
+    assert max_abs(got, ref) <= 2e-2
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_persistent_verify_row_blocks_with_early_returns(dtype):
     """Device lengths (the persistent grid), T = 4 with G = 3 (12 query rows: row blocks of
