@@ -78,6 +78,18 @@ def doc_block_mask(doc_ids: torch.Tensor):
     return create_block_mask(mask_mod, B, None, T, T, device=doc_ids.device)
 
 
+def causal_mask(T: int, S: int, offset: int, window: int, device) -> torch.Tensor:
+    """[T, S] bool, True = may attend: query t sits at position offset + t, key s at s; keys
+    after the query are hidden, and with a window those window or more positions before it
+    (attention.py:160-169)."""
+    qpos = torch.arange(T, device=device)[:, None] + offset
+    kpos = torch.arange(S, device=device)[None, :]
+    mask = kpos <= qpos
+    if window:
+        mask &= qpos - kpos < window
+    return mask
+
+
 def _is_block_mask(m) -> bool:
     """A FlexAttention BlockMask (anything but a tensor) in place of the bool same_doc mask."""
     return m is not None and not isinstance(m, torch.Tensor)
@@ -402,12 +414,7 @@ class Attention(nn.Module):
 
     def _mask(self, T: int, S: int, offset: int, device) -> torch.Tensor:
         """[T, S] bool, True = may attend (attention.py:160-169)."""
-        qpos = torch.arange(T, device=device)[:, None] + offset
-        kpos = torch.arange(S, device=device)[None, :]
-        mask = kpos <= qpos
-        if self.window:
-            mask &= qpos - kpos < self.window
-        return mask
+        return causal_mask(T, S, offset, self.window, device)
 
     def _fused(self, q, k, v, offset, same_doc=None):
         T, S = q.shape[2], k.shape[2]

@@ -19,7 +19,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from .attention import DECODE_MAX_T, _hip_ready, hip_shape_ok, hip_disabled
+from .attention import DECODE_MAX_T, _hip_ready, causal_mask, hip_shape_ok, hip_disabled
 from .norm import RMSNorm
 from .rope import apply_rope
 
@@ -93,11 +93,7 @@ class GatedAttention(nn.Module):
         if cache is not None:
             offset = cache.pos
             k, v = cache.update(self.layer_idx, k, v)
-        S = k.shape[2]
-        if T == 1:
-            mask = None
-        else:
-            qpos = torch.arange(T, device=q.device)[:, None] + offset
-            mask = torch.arange(S, device=q.device)[None, :] <= qpos
+        # one token sees the whole cache: no mask
+        mask = None if T == 1 else causal_mask(T, k.shape[2], offset, 0, q.device)
         return F.scaled_dot_product_attention(q, k.to(q.dtype), v.to(q.dtype), attn_mask=mask,
                                               enable_gqa=c.n_kv_heads != c.n_heads)
